@@ -1,0 +1,145 @@
+/*
+ * gdn_hip.h -- C ABI of libgdn_hip.so, the MI355X (gfx950) kernels of the
+ * Gated DeltaNet linear-attention path.
+ *
+ * Every entry point takes device pointers wrapped in plain tensor descriptors
+ * (pointer, dtype, shape, element strides), launches on the caller's HIP
+ * stream, never allocates, never synchronises the host and keeps no global
+ * mutable state.  Return value: 0 on success, > 0 a hipError_t from the
+ * launch, < 0 a validation code (nothing was launched).  gdn_strerror() maps
+ * any code to text.
+ *
+ * Index semantics shared by all entry points:
+ *  - state / conv-state slot indices are int32 or int64; a slot outside
+ *    [0, num_slots) marks a padding sequence: its output rows are zero and no
+ *    state is read or written.  Slots of one call must be distinct.
+ *  - cu_seqlens is int32 or int64, length N+1, non-decreasing, cu[0] = 0,
+ *    cu[N] <= T.  Kernels clamp every sequence range to [0, T].
+ *
+ * Reference interface (paths relative to yuyifanbupt/myvllm src/myvllm):
+ *  - gdn_recurrent_step   <- recurrent_gated_delta_rule,
+ *                            ops/gated_delta_rule/gated_delta_rule.py:69-92
+ *                            (kernel ops/gated_delta_rule/fused_recurrent_gdn.py:105-166)
+ *  - gdn_chunk_prefill    <- chunk_gated_delta_rule,
+ *                            ops/gated_delta_rule/gated_delta_rule.py:31-66
+ *  - causal_conv1d_varlen <- causal_conv1d_fn, ops/causal_conv1d.py:221-273
+ *  - causal_conv1d_step   <- causal_conv1d_update, ops/causal_conv1d.py:434-470
+ */
+#ifndef GDN_HIP_H_
+#define GDN_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+/* element types */
+#define GDN_DTYPE_F32 0
+#define GDN_DTYPE_BF16 1
+#define GDN_DTYPE_F16 2
+#define GDN_DTYPE_I32 3
+#define GDN_DTYPE_I64 4
+
+/* validation codes (negative); positive codes are hipError_t values */
+#define GDN_OK 0
+#define GDN_ERR_NULL (-1)       /* missing descriptor or data pointer */
+#define GDN_ERR_NDIM (-2)       /* wrong number of dimensions */
+#define GDN_ERR_SHAPE (-3)      /* shapes disagree with each other */
+#define GDN_ERR_DTYPE (-4)      /* unsupported element type */
+#define GDN_ERR_STRIDE (-5)     /* innermost stride must be 1 (state: [K][V] contiguous) */
+#define GDN_ERR_HEADS (-6)      /* num_v_heads not a positive multiple of num_k_heads */
+#define GDN_ERR_HEAD_DIM (-7)   /* head dims not supported by the kernels */
+#define GDN_ERR_CHUNK (-8)      /* chunk size not supported */
+#define GDN_ERR_ALIGN (-9)      /* pointer/stride misaligned for 16-byte vector access */
+#define GDN_ERR_CONV_WIDTH (-10) /* conv width outside [2, 6] */
+#define GDN_ERR_RANGE (-11)     /* a size exceeds the kernels' index range */
+
+#define GDN_MAX_NDIM 4
+
+typedef struct gdn_tensor {
+  void* data;                    /* device pointer (may be NULL only if numel == 0) */
+  int32_t dtype;                 /* GDN_DTYPE_* */
+  int32_t ndim;                  /* 1..4 */
+  int64_t shape[GDN_MAX_NDIM];   /* sizes */
+  int64_t stride[GDN_MAX_NDIM];  /* strides in elements */
+} gdn_tensor;
+
+/*
+ * Fused recurrent decode step, one token per sequence (replaces
+ * recurrent_gated_delta_rule, ops/gated_delta_rule/gated_delta_rule.py:69-92).
+ *   q, k   : (B, Hk, K)  bf16|f16|f32, last stride 1
+ *   v      : (B, Hv, V)  same dtype as q
+ *   g      : (B, Hv)     f32|bf16|f16   natural-log decay
+ *   beta   : (B, Hv)     f32|bf16|f16
+ *   state  : (S, Hv, K, V) f32, [K][V] contiguous per head; updated in place
+ *   state_indices : (B,) i32|i64
+ *   out    : (B, Hv, V)  bf16|f16|f32, last stride 1
+ * Per (b, h): S <- e^g S; d = beta (v - S^T k); S += k d^T; o = S^T (scale q).
+ * Supported head dims: K = V = 128 or K = V = 64.
+ */
+int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                       const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                       const gdn_tensor* state_indices, gdn_tensor* out, float scale,
+                       void* stream);
+
+/*
+ * Chunked gated-delta-rule prefill over packed varlen sequences (replaces
+ * chunk_gated_delta_rule, ops/gated_delta_rule/gated_delta_rule.py:31-66).
+ *   q, k   : (T, Hk, K)  bf16, last stride 1, token/head strides multiples of 8
+ *   v      : (T, Hv, V)  bf16, same constraints
+ *   g      : (T, Hv)     f32   natural-log decay per token and v-head
+ *   beta   : (T, Hv)     f32|bf16|f16
+ *   state  : (S, Hv, K, V) f32; initial state read from state[idx[n]], final
+ *            state written back there
+ *   state_indices : (N,) i32|i64
+ *   cu_seqlens    : (N+1,) i32|i64
+ *   out    : (T, Hv, V)  bf16, last stride 1
+ * chunk_size must be 64; K = V = 128.  Tokens not covered by any sequence
+ * keep whatever `out` held.
+ */
+int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                      const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                      const gdn_tensor* state_indices, const gdn_tensor* cu_seqlens,
+                      gdn_tensor* out, float scale, int32_t chunk_size, void* stream);
+
+/*
+ * Varlen depthwise causal conv1d + SiLU with conv-state carry-in/out
+ * (replaces causal_conv1d_fn, ops/causal_conv1d.py:221-273).
+ *   x          : (T, D) bf16|f16|f32, last stride 1
+ *   weight     : (D, W) same dtype as x or f32, any strides, 2 <= W <= 6
+ *   conv_state : (S, W-1, D) f32|bf16|f16, last stride 1; rows oldest first
+ *   conv_state_indices : (N,) i32|i64
+ *   cu_seqlens : (N+1,) i32|i64
+ *   out        : (T, D) same dtype as x, last stride 1
+ * y_t = silu(sum_j w[:, j] * xt[t + j]) over xt = [conv_state[slot]; x_seq];
+ * conv_state[slot] <- last W-1 rows of xt.  D must be a multiple of 8.
+ */
+int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                         const gdn_tensor* conv_state_indices, const gdn_tensor* cu_seqlens,
+                         gdn_tensor* out, void* stream);
+
+/*
+ * Single-token decode conv update (replaces causal_conv1d_update,
+ * ops/causal_conv1d.py:434-470).
+ *   x : (B, D); out : (B, D); other tensors as for causal_conv1d_varlen.
+ * y = silu(sum_j w[:, j] * xt[j]) over xt = [conv_state[slot]; x_b];
+ * conv_state[slot] <- xt[1:].
+ */
+int causal_conv1d_step(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                       const gdn_tensor* conv_state_indices, gdn_tensor* out, void* stream);
+
+/* Text for any return code of this library. */
+const char* gdn_strerror(int code);
+
+/* GDN_ABI_VERSION of the built library. */
+int gdn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_HIP_H_ */

@@ -1,0 +1,234 @@
+// C ABI of libgdn_hip.so: host-side validation and dispatch.
+//
+// Every check runs before any HIP call, so a malformed call returns a
+// negative code without touching the device (and these paths are testable on
+// a machine with no GPU).  The reference ops validate nothing beyond a few
+// asserts (ops/gated_delta_rule/solve_tril.py:98, ops/gated_delta_rule/h.py:211).
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#include "../../include/gdn_hip.h"
+
+hipError_t gdn_recurrent_step_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                                     const gdn_tensor* idx, gdn_tensor* out, float scale, hipStream_t st);
+hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                    const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                                    const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
+                                    hipStream_t st);
+hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
+                                       const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
+                                       hipStream_t st);
+hipError_t causal_conv1d_step_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
+                                     const gdn_tensor* idx, gdn_tensor* out, hipStream_t st);
+
+#define GDN_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+constexpr int64_t kMaxGrid = 2147483647;
+
+int64_t numel(const gdn_tensor* t) {
+  int64_t n = 1;
+  for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+  return n;
+}
+
+int elem_size(int dt) {
+  switch (dt) {
+    case GDN_DTYPE_F32: case GDN_DTYPE_I32: return 4;
+    case GDN_DTYPE_BF16: case GDN_DTYPE_F16: return 2;
+    case GDN_DTYPE_I64: return 8;
+    default: return 0;
+  }
+}
+
+bool is_float(int dt) { return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16; }
+bool is_index(int dt) { return dt == GDN_DTYPE_I32 || dt == GDN_DTYPE_I64; }
+
+// descriptor present, rank as expected, sizes non-negative, data present when non-empty
+int check_desc(const gdn_tensor* t, int ndim) {
+  if (!t) return GDN_ERR_NULL;
+  if (t->ndim != ndim) return GDN_ERR_NDIM;
+  for (int i = 0; i < ndim; ++i)
+    if (t->shape[i] < 0) return GDN_ERR_SHAPE;
+  if (elem_size(t->dtype) == 0) return GDN_ERR_DTYPE;
+  if (numel(t) > 0 && !t->data) return GDN_ERR_NULL;
+  return GDN_OK;
+}
+
+bool aligned(const gdn_tensor* t, int bytes) {
+  return (reinterpret_cast<uintptr_t>(t->data) % (uintptr_t)bytes) == 0;
+}
+
+// 16-byte vectors along the last dim: pointer aligned and every outer stride a
+// whole number of vectors.
+bool vec_ok(const gdn_tensor* t, int vec_bytes) {
+  const int es = elem_size(t->dtype);
+  if (!aligned(t, vec_bytes)) return false;
+  for (int i = 0; i + 1 < t->ndim; ++i)
+    if ((t->stride[i] * es) % vec_bytes != 0) return false;
+  return true;
+}
+
+#define GDN_TRY(expr)          \
+  do {                         \
+    int rc_ = (expr);          \
+    if (rc_ != GDN_OK) return rc_; \
+  } while (0)
+
+int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v, const gdn_tensor* g,
+                    const gdn_tensor* beta, const gdn_tensor* state, const gdn_tensor* idx,
+                    const gdn_tensor* out, const gdn_tensor* cu, bool prefill) {
+  GDN_TRY(check_desc(q, 3));
+  GDN_TRY(check_desc(k, 3));
+  GDN_TRY(check_desc(v, 3));
+  GDN_TRY(check_desc(g, 2));
+  GDN_TRY(check_desc(beta, 2));
+  GDN_TRY(check_desc(state, 4));
+  GDN_TRY(check_desc(idx, 1));
+  GDN_TRY(check_desc(out, 3));
+  if (prefill) GDN_TRY(check_desc(cu, 1));
+
+  const int64_t T = q->shape[0], Hk = q->shape[1], K = q->shape[2];
+  const int64_t Hv = v->shape[1], V = v->shape[2];
+  for (int i = 0; i < 3; ++i)
+    if (k->shape[i] != q->shape[i]) return GDN_ERR_SHAPE;
+  if (v->shape[0] != T || out->shape[0] != T || out->shape[1] != Hv || out->shape[2] != V) return GDN_ERR_SHAPE;
+  if (g->shape[0] != T || g->shape[1] != Hv || beta->shape[0] != T || beta->shape[1] != Hv) return GDN_ERR_SHAPE;
+  if (state->shape[1] != Hv || state->shape[2] != K || state->shape[3] != V) return GDN_ERR_SHAPE;
+  if (prefill) {
+    if (cu->shape[0] < 1 || idx->shape[0] != cu->shape[0] - 1) return GDN_ERR_SHAPE;
+  } else {
+    if (idx->shape[0] != T) return GDN_ERR_SHAPE;
+  }
+  if (Hk <= 0 || Hv % Hk != 0) return GDN_ERR_HEADS;
+
+  // dtypes
+  if (k->dtype != q->dtype || v->dtype != q->dtype || out->dtype != v->dtype) return GDN_ERR_DTYPE;
+  if (!is_float(q->dtype) || !is_float(g->dtype) || !is_float(beta->dtype)) return GDN_ERR_DTYPE;
+  if (state->dtype != GDN_DTYPE_F32 || !is_index(idx->dtype)) return GDN_ERR_DTYPE;
+  if (prefill && (q->dtype != GDN_DTYPE_BF16 || g->dtype != GDN_DTYPE_F32 || !is_index(cu->dtype)))
+    return GDN_ERR_DTYPE;
+
+  // head dims
+  if (prefill) {
+    if (K != 128 || V != 128) return GDN_ERR_HEAD_DIM;
+  } else {
+    if (!((K == 128 && V == 128) || (K == 64 && V == 64))) return GDN_ERR_HEAD_DIM;
+  }
+
+  // strides
+  if (q->stride[2] != 1 || k->stride[2] != 1 || v->stride[2] != 1 || out->stride[2] != 1) return GDN_ERR_STRIDE;
+  if (state->stride[3] != 1 || state->stride[2] != V) return GDN_ERR_STRIDE;
+  if (idx->stride[0] != 1 || (prefill && cu->stride[0] != 1)) return GDN_ERR_STRIDE;
+
+  // alignment: fp32 state rows as 16-byte vectors; prefill q/k/v/out as 16-byte vectors
+  if (T > 0 && !vec_ok(state, 16)) return GDN_ERR_ALIGN;
+  if (prefill && T > 0) {
+    if (!vec_ok(q, 16) || !vec_ok(k, 16) || !vec_ok(v, 16) || !vec_ok(out, 16)) return GDN_ERR_ALIGN;
+  }
+
+  // index ranges
+  if (prefill) {
+    if (idx->shape[0] * Hv > kMaxGrid || T > kMaxGrid) return GDN_ERR_RANGE;
+  } else {
+    if (T * Hv > kMaxGrid) return GDN_ERR_RANGE;
+  }
+  return GDN_OK;
+}
+
+int check_conv(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, const gdn_tensor* idx,
+               const gdn_tensor* cu, const gdn_tensor* out, bool varlen) {
+  GDN_TRY(check_desc(x, 2));
+  GDN_TRY(check_desc(w, 2));
+  GDN_TRY(check_desc(cs, 3));
+  GDN_TRY(check_desc(idx, 1));
+  GDN_TRY(check_desc(out, 2));
+  if (varlen) GDN_TRY(check_desc(cu, 1));
+
+  const int64_t T = x->shape[0], D = x->shape[1], W = w->shape[1];
+  if (W < 2 || W > 6) return GDN_ERR_CONV_WIDTH;
+  if (w->shape[0] != D || cs->shape[1] != W - 1 || cs->shape[2] != D) return GDN_ERR_SHAPE;
+  if (out->shape[0] != T || out->shape[1] != D) return GDN_ERR_SHAPE;
+  if (varlen) {
+    if (cu->shape[0] < 1 || idx->shape[0] != cu->shape[0] - 1) return GDN_ERR_SHAPE;
+  } else {
+    if (idx->shape[0] != T) return GDN_ERR_SHAPE;
+  }
+  if (D % 8 != 0) return GDN_ERR_SHAPE;
+
+  if (!is_float(x->dtype) || out->dtype != x->dtype) return GDN_ERR_DTYPE;
+  if (w->dtype != x->dtype && w->dtype != GDN_DTYPE_F32) return GDN_ERR_DTYPE;
+  if (cs->dtype != x->dtype && cs->dtype != GDN_DTYPE_F32) return GDN_ERR_DTYPE;
+  if (!is_index(idx->dtype) || (varlen && !is_index(cu->dtype))) return GDN_ERR_DTYPE;
+
+  if (x->stride[1] != 1 || out->stride[1] != 1 || cs->stride[2] != 1) return GDN_ERR_STRIDE;
+  if (idx->stride[0] != 1 || (varlen && cu->stride[0] != 1)) return GDN_ERR_STRIDE;
+
+  if (T > 0 && D > 0) {
+    if (!vec_ok(x, 16) || !vec_ok(out, 16)) return GDN_ERR_ALIGN;
+    if (!vec_ok(cs, 16)) return GDN_ERR_ALIGN;
+  }
+  if (T > kMaxGrid || D / 8 > kMaxGrid) return GDN_ERR_RANGE;
+  return GDN_OK;
+}
+
+int launch_rc(hipError_t e) { return e == hipSuccess ? GDN_OK : (int)e; }
+
+}  // namespace
+
+GDN_EXPORT int gdn_abi_version(void) { return GDN_ABI_VERSION; }
+
+GDN_EXPORT const char* gdn_strerror(int code) {
+  switch (code) {
+    case GDN_OK: return "success";
+    case GDN_ERR_NULL: return "missing tensor descriptor or data pointer";
+    case GDN_ERR_NDIM: return "tensor has the wrong number of dimensions";
+    case GDN_ERR_SHAPE: return "tensor shapes are inconsistent";
+    case GDN_ERR_DTYPE: return "unsupported tensor dtype";
+    case GDN_ERR_STRIDE: return "unsupported strides (innermost dims must be contiguous)";
+    case GDN_ERR_HEADS: return "num_v_heads must be a positive multiple of num_k_heads";
+    case GDN_ERR_HEAD_DIM: return "unsupported head dims";
+    case GDN_ERR_CHUNK: return "unsupported chunk size (64 required)";
+    case GDN_ERR_ALIGN: return "pointer or stride misaligned for 16-byte vector access";
+    case GDN_ERR_CONV_WIDTH: return "conv width must be in [2, 6]";
+    case GDN_ERR_RANGE: return "size exceeds the kernels' index range";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "unknown error code";
+}
+
+GDN_EXPORT int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                  const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                                  const gdn_tensor* state_indices, gdn_tensor* out, float scale, void* stream) {
+  GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, nullptr, false));
+  return launch_rc(gdn_recurrent_step_launch(q, k, v, g, beta, state, state_indices, out, scale,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                 const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                                 const gdn_tensor* state_indices, const gdn_tensor* cu_seqlens,
+                                 gdn_tensor* out, float scale, int32_t chunk_size, void* stream) {
+  if (chunk_size != 64) return GDN_ERR_CHUNK;
+  GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, cu_seqlens, true));
+  return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale,
+                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                                    const gdn_tensor* conv_state_indices, const gdn_tensor* cu_seqlens,
+                                    gdn_tensor* out, void* stream) {
+  GDN_TRY(check_conv(x, weight, conv_state, conv_state_indices, cu_seqlens, out, true));
+  return launch_rc(causal_conv1d_varlen_launch(x, weight, conv_state, conv_state_indices, cu_seqlens, out,
+                                               reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int causal_conv1d_step(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                                  const gdn_tensor* conv_state_indices, gdn_tensor* out, void* stream) {
+  GDN_TRY(check_conv(x, weight, conv_state, conv_state_indices, nullptr, out, false));
+  return launch_rc(causal_conv1d_step_launch(x, weight, conv_state, conv_state_indices, out,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}

@@ -1,0 +1,154 @@
+// Shared device helpers for the gfx950 kernels of libgdn_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gdn_hip.h"
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define GDN_DEVICE __device__ __forceinline__
+
+// ---- scalar conversions -------------------------------------------------
+GDN_DEVICE float to_f32(float x) { return x; }
+GDN_DEVICE float to_f32(bf16_t x) { return (float)x; }
+GDN_DEVICE float to_f32(f16_t x) { return (float)x; }
+
+template <typename T> GDN_DEVICE T from_f32(float x);
+template <> GDN_DEVICE float from_f32<float>(float x) { return x; }
+template <> GDN_DEVICE bf16_t from_f32<bf16_t>(float x) { return (bf16_t)x; }  // RNE (v_cvt_pk_bf16_f32)
+template <> GDN_DEVICE f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
+
+// ---- 8-wide vector load/store of any element type as fp32 -----------------
+// p must be 16-byte aligned for 2-byte types and 32-byte aligned for fp32
+// (the host checks pointer and stride alignment before launch).
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16_t> {
+  static GDN_DEVICE void load(const bf16_t* p, float* f) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+  }
+  static GDN_DEVICE void store(bf16_t* p, const float* f) {
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (bf16_t)f[i];
+    *reinterpret_cast<bf16x8*>(p) = v;
+  }
+};
+template <> struct Vec8<f16_t> {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  static GDN_DEVICE void load(const f16_t* p, float* f) {
+    h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+  }
+  static GDN_DEVICE void store(f16_t* p, const float* f) {
+    h8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (f16_t)f[i];
+    *reinterpret_cast<h8*>(p) = v;
+  }
+};
+template <> struct Vec8<float> {
+  static GDN_DEVICE void load(const float* p, float* f) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
+  }
+  static GDN_DEVICE void store(float* p, const float* f) {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] = f[i]; b[i] = f[4 + i]; }
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+};
+
+// Scalar of a runtime-typed float tensor (used for per-row scalars like g, beta).
+GDN_DEVICE float load_scalar_f32(const void* p, int64_t off, int dtype) {
+  switch (dtype) {
+    case GDN_DTYPE_BF16: return (float)reinterpret_cast<const bf16_t*>(p)[off];
+    case GDN_DTYPE_F16: return (float)reinterpret_cast<const f16_t*>(p)[off];
+    default: return reinterpret_cast<const float*>(p)[off];
+  }
+}
+
+// ---- index tensors (int32 or int64) ----------------------------------------
+GDN_DEVICE int64_t load_index(const void* p, int64_t i, bool is64) {
+  return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+// Sequence n of a packed batch, clamped to [0, T] and to a non-negative length.
+GDN_DEVICE void seq_range(const void* cu, bool cu64, int64_t n, int64_t T, int64_t& s, int64_t& e) {
+  int64_t a = load_index(cu, n, cu64);
+  int64_t b = load_index(cu, n + 1, cu64);
+  a = a < 0 ? 0 : (a > T ? T : a);
+  b = b < a ? a : (b > T ? T : b);
+  s = a;
+  e = b;
+}
+
+GDN_DEVICE float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+
+// Block-wide lookup of the (sequence, tile) pair owning linear tile id
+// `target`, where sequence n is cut into ceil(len_n / tile_len) tiles laid
+// out sequence after sequence.  Every thread of the (256-thread) block must
+// call it; all receive the same answer, seq = -1 when target is past the end.
+// `lds` must hold at least 6 int64 values.
+template <int NT>
+GDN_DEVICE void find_seq_tile(const void* cu, bool cu64, int64_t nseq, int64_t T, int tile_len, int64_t target,
+                              int64_t& seq, int64_t& tile, int64_t* lds) {
+  static_assert(NT == 256, "find_seq_tile assumes 256 threads");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid == 0) { lds[4] = -1; lds[5] = 0; }
+  int64_t running = 0;
+  for (int64_t base = 0; base < nseq; base += NT) {
+    const int64_t n = base + tid;
+    int64_t cnt = 0;
+    if (n < nseq) {
+      int64_t s, e;
+      seq_range(cu, cu64, n, T, s, e);
+      cnt = (e - s + tile_len - 1) / tile_len;
+    }
+    // inclusive scan inside the wave
+    int64_t incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      int64_t y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    __syncthreads();  // lds[0..3] free from the previous round
+    if (lane == 63) lds[wave] = incl;
+    __syncthreads();
+    int64_t wave_off = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      int64_t tw = lds[w];
+      if (w < wave) wave_off += tw;
+      total += tw;
+    }
+    const int64_t hi = running + wave_off + incl;
+    const int64_t lo = hi - cnt;
+    if (cnt > 0 && target >= lo && target < hi) {
+      lds[4] = n;
+      lds[5] = target - lo;
+    }
+    running += total;
+    __syncthreads();
+    if (lds[4] >= 0 || target < running) break;
+  }
+  seq = lds[4];
+  tile = lds[5];
+}

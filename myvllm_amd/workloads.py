@@ -1,0 +1,153 @@
+"""Seeded synthetic inputs for the GDN path's benchmark and parity workloads.
+
+Every tensor is drawn on the CPU from one ``torch.Generator().manual_seed(seed)``
+in a fixed order, so the CPU oracle and the GPU kernels see identical bits;
+callers copy to the device themselves.  Distributions follow the GDN layer's
+input contract (``layers/linear_attention.py:89-90``, ``:113-114`` of
+yuyifanbupt/myvllm): q, k ~ N(0, 1) then L2-normalised per head, v ~ N(0, 1),
+beta = sigmoid(N(0, 1)), g = -softplus(N(0, 1)).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+HK, HV, DK, DV = 16, 32, 128, 128
+CONV_DIM = 2 * HK * DK + HV * DV  # 8192 = q 2048 | k 2048 | v 4096
+CONV_WIDTH = 4
+
+
+def gdn_inputs(
+    gen: torch.Generator,
+    T: int,
+    Hk: int = HK,
+    Hv: int = HV,
+    K: int = DK,
+    V: int = DV,
+    dtype: torch.dtype = torch.bfloat16,
+    beta_dtype: torch.dtype = torch.float32,
+    g_scale: float = 1.0,
+):
+    """q, k, v (rounded once to ``dtype``), g (fp32), beta, in that draw order."""
+    q = F.normalize(torch.randn(T, Hk, K, generator=gen), dim=-1).to(dtype)
+    k = F.normalize(torch.randn(T, Hk, K, generator=gen), dim=-1).to(dtype)
+    v = torch.randn(T, Hv, V, generator=gen).to(dtype)
+    g = -F.softplus(torch.randn(T, Hv, generator=gen)) * g_scale
+    beta = torch.sigmoid(torch.randn(T, Hv, generator=gen)).to(beta_dtype)
+    return q, k, v, g, beta
+
+
+def cu_from_lengths(lengths) -> torch.Tensor:
+    lens = torch.as_tensor(lengths, dtype=torch.int64)
+    return torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)]).to(torch.int32)
+
+
+@dataclass
+class PrefillCase:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    g: torch.Tensor
+    beta: torch.Tensor
+    state: torch.Tensor  # (num_slots, Hv, K, V) fp32
+    idx: torch.Tensor  # (N,) int32
+    cu: torch.Tensor  # (N+1,) int32
+
+    @property
+    def tokens(self) -> int:
+        return int(self.cu[-1])
+
+
+def prefill_case(
+    lengths,
+    seed: int = 0,
+    num_slots: int | None = None,
+    Hk: int = HK,
+    Hv: int = HV,
+    state_std: float = 0.1,
+    g_scale: float = 1.0,
+    beta_dtype: torch.dtype = torch.float32,
+) -> PrefillCase:
+    """Chunked-prefill inputs for given sequence lengths (draws after the lengths)."""
+    gen = torch.Generator().manual_seed(seed)
+    N = len(lengths)
+    cu = cu_from_lengths(lengths)
+    T = int(cu[-1])
+    q, k, v, g, beta = gdn_inputs(gen, T, Hk, Hv, beta_dtype=beta_dtype, g_scale=g_scale)
+    num_slots = num_slots or max(N, 1)
+    state = torch.randn(num_slots, Hv, DK, DV, generator=gen) * state_std
+    idx = torch.randperm(num_slots, generator=gen)[:N].to(torch.int32)
+    return PrefillCase(q, k, v, g, beta, state, idx, cu)
+
+
+def prefill_32k_case(seed: int = 0) -> PrefillCase:
+    """Chunked GDN prefill workload: 16 sequences, lengths uniform in [512, 4096]
+    (seed 0: 35,846 tokens, 567 chunks of 64), Hk 16 / Hv 32, d 128, bf16 q/k/v,
+    fp32 g/beta, fp32 initial state ~N(0, 0.1) in a 64-slot cache."""
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(512, 4097, (16,), generator=gen).tolist()
+    return prefill_case(lengths, seed=seed + 1, num_slots=64)
+
+
+@dataclass
+class DecodeCase:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    g: torch.Tensor
+    beta: torch.Tensor
+    state: torch.Tensor  # (num_slots, Hv, K, V) fp32
+    idx: torch.Tensor  # (B,) int32
+
+
+def decode_case(B: int = 256, num_slots: int = 1024, seed: int = 0, Hk: int = HK, Hv: int = HV,
+                K: int = DK, V: int = DV, dtype=torch.bfloat16, beta_dtype=torch.float32,
+                state: bool = True) -> DecodeCase:
+    """Recurrent decode workload: B sequences x 1 token, fp32 state cache
+    (num_slots, Hv, K, V) ~N(0, 0.1), slots = randperm(num_slots)[:B].
+    With ``state=False`` the cache is left for the caller to fill (used by
+    the benchmark to build the 2 GiB cache on the device)."""
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v, g, beta = gdn_inputs(gen, B, Hk, Hv, K, V, dtype=dtype, beta_dtype=beta_dtype)
+    idx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
+    st = torch.randn(num_slots, Hv, K, V, generator=gen) * 0.1 if state else None
+    return DecodeCase(q, k, v, g, beta, st, idx)
+
+
+@dataclass
+class ConvCase:
+    x: torch.Tensor
+    weight: torch.Tensor
+    state: torch.Tensor
+    idx: torch.Tensor
+    cu: torch.Tensor | None
+
+
+def conv_prefill_case(lengths=None, seed: int = 0, D: int = CONV_DIM, W: int = CONV_WIDTH, num_slots: int = 1024,
+                      dtype=torch.bfloat16, state_dtype=torch.float32) -> ConvCase:
+    """Varlen conv workload: by default 8 sequences, lengths uniform in [256, 4096]
+    (seed 0: [2943, 3503, 2192, 1807, 3696, 649, 3521, 1451], 19,762 tokens),
+    8192 channels, width 4, x and w ~N(0, 0.02) bf16, no bias, fp32 conv state."""
+    gen = torch.Generator().manual_seed(seed)
+    if lengths is None:
+        lengths = torch.randint(256, 4097, (8,), generator=gen).tolist()
+    cu = cu_from_lengths(lengths)
+    T = int(cu[-1])
+    x = (torch.randn(T, D, generator=gen) * 0.02).to(dtype)
+    w = (torch.randn(D, W, generator=gen) * 0.02).to(dtype)
+    st = (torch.randn(num_slots, W - 1, D, generator=gen) * 0.02).to(dtype).to(state_dtype)
+    idx = torch.randperm(num_slots, generator=gen)[: len(lengths)].to(torch.int32)
+    return ConvCase(x, w, st, idx, cu)
+
+
+def conv_decode_case(B: int = 256, seed: int = 0, D: int = CONV_DIM, W: int = CONV_WIDTH, num_slots: int = 1024,
+                     dtype=torch.bfloat16, state_dtype=torch.float32) -> ConvCase:
+    """Decode conv workload: B tokens, width-W conv state per slot (fp32), 1024 slots."""
+    gen = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, D, generator=gen) * 0.02).to(dtype)
+    w = (torch.randn(D, W, generator=gen) * 0.02).to(dtype)
+    st = (torch.randn(num_slots, W - 1, D, generator=gen) * 0.02).to(dtype).to(state_dtype)
+    idx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
+    return ConvCase(x, w, st, idx, None)
