@@ -1,0 +1,114 @@
+"""GPU parity: fused chunked prefill vs the CPU oracle (chunked UT form in fp64)."""
+import pytest
+import torch
+
+from conftest import assert_out_close, assert_state_close
+from myvllm_amd import chunk_gated_delta_rule, chunk_gated_delta_rule_fwd, recurrent_gated_delta_rule
+from myvllm_amd.workloads import cu_from_lengths, prefill_32k_case, prefill_case
+from oracle.gdn import chunk_gated_delta_rule_ref, recurrent_gated_delta_rule_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(case, dev, idx=None, cu=None, beta=None):
+    idx = case.idx if idx is None else idx
+    cu = case.cu if cu is None else cu
+    beta = case.beta if beta is None else beta
+    st_ref = case.state.clone()
+    o_ref = chunk_gated_delta_rule_ref(case.q, case.k, case.v, case.g, beta, st_ref, idx, cu)
+    st = case.state.to(dev)
+    o = chunk_gated_delta_rule(
+        case.q.to(dev), case.k.to(dev), case.v.to(dev), case.g.to(dev), beta.to(dev), st, idx.to(dev), cu.to(dev)
+    )
+    torch.cuda.synchronize()
+    return o.cpu(), st.cpu(), o_ref, st_ref
+
+
+def _check(case, o, st, o_ref, st_ref, idx=None):
+    idx = case.idx if idx is None else idx
+    assert_out_close(o, o_ref)
+    sel = torch.tensor([int(i) for i in idx.tolist() if 0 <= int(i) < st.shape[0]], dtype=torch.long)
+    assert_state_close(st[sel], st_ref[sel])
+    untouched = torch.ones(st.shape[0], dtype=torch.bool)
+    untouched[sel] = False
+    assert torch.equal(st[untouched], case.state[untouched])
+
+
+@pytest.mark.parametrize("lengths", [[64], [1], [5, 64, 65], [130, 0, 200, 3, 127, 128, 129]])
+def test_prefill_varlen_edges(dev, lengths):
+    case = prefill_case(lengths, seed=len(lengths), num_slots=len(lengths) + 3, Hk=2, Hv=4)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_gva_ratio_one_and_four(dev):
+    for Hk, Hv in ((4, 4), (1, 4)):
+        case = prefill_case([70, 33], seed=7, num_slots=4, Hk=Hk, Hv=Hv)
+        o, st, o_ref, st_ref = _run(case, dev)
+        _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_weak_decay(dev):
+    """g scaled by 0.01: the state carries across chunks, stressing the split-bf16 products."""
+    case = prefill_case([300, 1000], seed=8, num_slots=2, Hk=2, Hv=4, g_scale=0.01)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_zero_decay_beta_one(dev):
+    """g = 0, beta = 1: pure delta rule, no decay at all."""
+    case = prefill_case([256], seed=9, num_slots=1, Hk=1, Hv=2)
+    case.g.zero_()
+    case.beta.fill_(1.0)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_padding_slot_int64_bf16_beta(dev):
+    case = prefill_case([40, 90, 17], seed=10, num_slots=5, Hk=2, Hv=4, beta_dtype=torch.bfloat16)
+    idx = case.idx.long().clone()
+    idx[1] = -1
+    o, st, o_ref, st_ref = _run(case, dev, idx=idx, cu=case.cu.long())
+    assert torch.count_nonzero(o[40:130]) == 0
+    _check(case, o, st, o_ref, st_ref, idx=idx)
+
+
+def test_prefill_split_equals_whole_and_decode_continues(dev):
+    """Prefill of 150 tokens == prefill 100 then 50 (carried state) == prefill 149 then one decode step."""
+    case = prefill_case([150], seed=11, num_slots=1, Hk=2, Hv=4)
+    q, k, v, g, b = (t.to(dev) for t in (case.q, case.k, case.v, case.g, case.beta))
+    idx = case.idx.to(dev)
+    st_a = case.state.to(dev)
+    o_a = chunk_gated_delta_rule(q, k, v, g, b, st_a, idx, cu_from_lengths([150]).to(dev))
+    st_b = case.state.to(dev)
+    o_b1 = chunk_gated_delta_rule(q[:100], k[:100], v[:100], g[:100], b[:100], st_b, idx, cu_from_lengths([100]).to(dev))
+    o_b2 = chunk_gated_delta_rule(q[100:], k[100:], v[100:], g[100:], b[100:], st_b, idx, cu_from_lengths([50]).to(dev))
+    st_c = case.state.to(dev)
+    o_c1 = chunk_gated_delta_rule(q[:149], k[:149], v[:149], g[:149], b[:149], st_c, idx, cu_from_lengths([149]).to(dev))
+    o_c2 = recurrent_gated_delta_rule(q[149:], k[149:], v[149:], g[149:], b[149:], st_c, idx)
+    assert_out_close(torch.cat([o_b1, o_b2]), o_a.float())
+    assert_out_close(torch.cat([o_c1, o_c2]), o_a.float())
+    assert_state_close(st_b, st_a)
+    assert_state_close(st_c, st_a)
+
+
+def test_prefill_functional_form(dev):
+    case = prefill_case([77, 10], seed=12, num_slots=2, Hk=2, Hv=4)
+    init = case.state[case.idx.long()]
+    o, fin = chunk_gated_delta_rule_fwd(
+        case.q.to(dev), case.k.to(dev), case.v.to(dev), case.g.to(dev), case.beta.to(dev), case.cu.to(dev),
+        initial_state=init.to(dev), output_final_state=True,
+    )
+    st_ref = init.clone()
+    o_ref = chunk_gated_delta_rule_ref(case.q, case.k, case.v, case.g, case.beta, st_ref,
+                                       torch.arange(2, dtype=torch.int32), case.cu)
+    assert_out_close(o, o_ref)
+    assert_state_close(fin, st_ref)
+
+
+def test_prefill_32k_full(dev):
+    """Benchmark shape: 16 sequences, 35,846 tokens, Hk 16 / Hv 32, d 128, fp32 initial state."""
+    case = prefill_32k_case()
+    assert case.tokens == 35846
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
