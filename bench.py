@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""Benchmark of the Gated DeltaNet path on one MI355X.
+
+Headline (the JSON line's ``value``): chunked gated-delta-rule prefill
+throughput in tokens/s on the 32k-token varlen workload (16 sequences,
+lengths uniform in [512, 4096] -> 35,846 tokens, Hk 16 / Hv 32, d 128,
+chunk 64, bf16 q/k/v, fp32 g/beta and state).  The same line carries the
+recurrent decode step (batch 256, fp32 state gathered from a 1024-slot
+cache, HBM GB/s), the varlen causal conv1d (8 sequences, 19,762 tokens,
+8192 channels, width 4) and the conv decode update (batch 256), each with
+its roofline and the CPU oracle timed on this host.
+
+A step is one call of the op on inputs already resident in HBM.  Timing:
+W untimed warm-up steps, then K steps bracketed by device synchronisation;
+per-launch kernel time from HIP events recorded on the stream the kernel is
+launched on.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+HK, HV, DK, DV, CHUNK = 16, 32, 128, 128, 64
+# algorithmic FLOPs per prefill token: KK^T and QK^T once per k-head (C x C x K),
+# per v-head w, u, A_qk v', w S, k^T v', q S (2 C V + C K + 3 K V), x2 for FMA
+PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK + 3 * DK * DV) * HV)
+
+
+def _cpu_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    n = int(env) if env and env.isdigit() else (os.cpu_count() or 1)
+    return max(1, min(n, 16))
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_gpu(fn, steps: int, warmup: int):
+    """Run fn() warmup + steps times; return (wall ms/step, mean kernel ms from per-step events)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(steps):
+        evs[i][0].record(stream)
+        fn(warmup + i)
+        evs[i][1].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total = t0.elapsed_time(t1)
+    per = [a.elapsed_time(b) for a, b in evs]
+    return total / steps, sum(per) / len(per)
+
+
+def _time_cpu(fn, budget_s: float, max_reps: int = 5):
+    fn()  # warm
+    reps, t_start = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t_start
+        if el >= budget_s or reps >= max_reps:
+            return el / reps
+
+
+def bench_prefill(dev, steps, warmup, cpu_budget):
+    from myvllm_amd import chunk_gated_delta_rule
+    from myvllm_amd.workloads import prefill_32k_case
+
+    case = prefill_32k_case()
+    T = case.tokens
+    q, k, v, g, beta, state, idx, cu = (t.to(dev) for t in (case.q, case.k, case.v, case.g, case.beta,
+                                                             case.state, case.idx, case.cu))
+
+    def step(_):
+        chunk_gated_delta_rule(q, k, v, g, beta, state, idx, cu)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    flop = PREFILL_FLOP_PER_TOKEN * T
+    achieved = flop / (kern_ms * 1e-3) / 1e12
+    res = {
+        "tokens": T,
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms,
+        "tokens_per_s": T / (ms * 1e-3),
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": None,
+                     "flop_per_launch": flop, "kernel": "gdn_chunk_prefill_kernel"},
+    }
+    if cpu_budget > 0:
+        from oracle.gdn import chunk_gated_delta_rule_ref
+
+        torch.set_num_threads(_cpu_threads())
+        st = case.state.clone()
+        sec = _time_cpu(lambda: chunk_gated_delta_rule_ref(case.q, case.k, case.v, case.g, case.beta, st, case.idx,
+                                                           case.cu, dtype=torch.float32), cpu_budget)
+        res["cpu_baseline"] = {"value": T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"full workload ({T} tokens), fp32 chunked (C=64) torch restatement, "
+                                         f"{_cpu_model()}"}
+    return res
+
+
+def bench_decode(dev, steps, warmup, cpu_budget):
+    from myvllm_amd import recurrent_gated_delta_rule
+    from myvllm_amd.workloads import decode_case
+
+    B, slots = 256, 1024
+    case = decode_case(B=B, num_slots=slots, seed=0, state=False)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    state = torch.randn(slots, HV, DK, DV, device=dev, generator=gen) * 0.1
+    # 4 disjoint slot sets in rotation, so the 256 MB last-level cache cannot serve repeats
+    perm = torch.randperm(slots, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    idxs = [perm[i * B:(i + 1) * B].to(dev) for i in range(4)]
+    q, k, v, g, beta = (t.to(dev) for t in (case.q, case.k, case.v, case.g, case.beta))
+
+    def step(i):
+        recurrent_gated_delta_rule(q, k, v, g, beta, state, idxs[i % 4])
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    per_seq = 2 * HV * DK * DV * 4 + (2 * HK * DK + 2 * HV * DV) * 2 + 2 * HV * 4 + 4
+    nbytes = per_seq * B
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "batch": B,
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms,
+        "GB_per_s": gbs,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": None, "bytes_per_launch": nbytes, "kernel": "gdn_recurrent_step_kernel"},
+    }
+    if cpu_budget > 0:
+        from oracle.gdn import recurrent_gated_delta_rule_ref
+
+        torch.set_num_threads(_cpu_threads())
+        sub = 32  # bounded sample: 32 of the 256 sequences (64 MB of state)
+        st = torch.randn(sub, HV, DK, DV) * 0.1
+        sidx = torch.arange(sub, dtype=torch.int32)
+        sec = _time_cpu(lambda: recurrent_gated_delta_rule_ref(case.q[:sub], case.k[:sub], case.v[:sub], case.g[:sub],
+                                                               case.beta[:sub], st, sidx, dtype=torch.float32),
+                        cpu_budget)
+        res["cpu_baseline"] = {"value": per_seq * sub / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"{sub} of {B} sequences, fp32 token recurrence"}
+    return res
+
+
+def bench_conv(dev, steps, warmup, cpu_budget):
+    from myvllm_amd import causal_conv1d_fn
+    from myvllm_amd.workloads import CONV_DIM, CONV_WIDTH, conv_prefill_case
+
+    case = conv_prefill_case()
+    T, D, W, N = int(case.cu[-1]), CONV_DIM, CONV_WIDTH, case.cu.numel() - 1
+    x, w, st, idx, cu = (t.to(dev) for t in (case.x, case.weight, case.state, case.idx, case.cu))
+
+    def step(_):
+        causal_conv1d_fn(x, w, st, idx, cu)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    nbytes = 4 * T * D + 2 * D * W + 2 * N * (W - 1) * D * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    res = {"tokens": T, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
+                        "kernel": "causal_conv1d_varlen_kernel"}}
+    if cpu_budget > 0:
+        from oracle.conv import causal_conv1d_fn_ref
+
+        torch.set_num_threads(_cpu_threads())
+        cst = case.state.clone()
+        sec = _time_cpu(lambda: causal_conv1d_fn_ref(case.x, case.weight, cst, case.idx, case.cu, dtype=torch.float32),
+                        cpu_budget)
+        res["cpu_baseline"] = {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": "full workload, fp32 F.conv1d + SiLU per sequence"}
+    return res
+
+
+def bench_conv_update(dev, steps, warmup, cpu_budget):
+    from myvllm_amd import causal_conv1d_update
+    from myvllm_amd.workloads import CONV_DIM, CONV_WIDTH, conv_decode_case
+
+    case = conv_decode_case()
+    B, D, W = case.x.shape[0], CONV_DIM, CONV_WIDTH
+    x, w, st = (t.to(dev) for t in (case.x, case.weight, case.state))
+    perm = torch.randperm(1024, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    idxs = [perm[i * B:(i + 1) * B].to(dev) for i in range(4)]
+
+    def step(i):
+        causal_conv1d_update(x, w, st, idxs[i % 4])
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    nbytes = 4 * B * D + 2 * D * W + 2 * B * (W - 1) * D * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
+                         "kernel": "causal_conv1d_step_kernel"}}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update"], default="all")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time budget of each CPU-oracle baseline (0 disables it)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the GDN path is benchmarked on a single MI355X "
+              "(the kernels shard over heads/sequences with no communication; see the design notes). "
+              "Run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    parts = {}
+    want = (lambda w: args.workload in ("all", w))
+    if want("prefill"):
+        parts["prefill"] = bench_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# prefill: {parts['prefill']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if want("decode"):
+        parts["decode"] = bench_decode(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# decode: {parts['decode']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if want("conv"):
+        parts["conv"] = bench_conv(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# conv: {parts['conv']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if want("conv_update"):
+        parts["conv_update"] = bench_conv_update(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# conv_update: {parts['conv_update']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+
+    head_name = "prefill" if "prefill" in parts else next(iter(parts))
+    head = parts.pop(head_name)
+    if head_name == "prefill":
+        metric, value, unit = "GDN prefill tokens/s", head["tokens_per_s"], "tokens/s"
+        workload = (f"gdn_chunk_prefill: 16 varlen seqs (lengths U[512,4096], seed 0), {head['tokens']} tokens, "
+                    f"Hk {HK} / Hv {HV}, d {DK}, chunk {CHUNK}, bf16 q/k/v, fp32 g/beta/state")
+    elif head_name == "decode":
+        metric, value, unit = "GDN decode state-update HBM GB/s", head["GB_per_s"], "GB/s"
+        workload = "gdn_recurrent_step: batch 256 from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128"
+    else:
+        metric, value, unit = f"causal_conv1d {head_name} HBM GB/s", head["GB_per_s"], "GB/s"
+        workload = f"causal_conv1d {head_name}: 8192 channels, width 4, bf16 x/w, fp32 conv state"
+    line = {
+        "metric": metric,
+        "value": value,
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.Generator, CPU-drawn, copied to HBM before timing)",
+        "config": {"workload": workload, "kernel_ms": head["kernel_ms"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+    }
+    for name, part in parts.items():
+        line[name] = part
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -7,32 +7,35 @@
 // 256-thread workgroup walks the chunks of one sequence for one v-head and
 // keeps everything on chip: the fp32 128x128 state lives in the registers of
 // its 4 waves (wave w owns value columns [32w, 32w+32)), the chunk's K/Q/V
-// tiles and the 64x64 chunk matrices live in LDS, and only q/k/v/g/beta are
-// read and o written.
+// tiles and the 64x64 chunk matrices live in LDS (< 80 KiB, so two
+// workgroups share a CU), and only q/k/v/g/beta are read and o written.
 //
 // Per chunk of L <= 64 tokens (gamma = in-chunk cumsum of g):
-//   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kkt, bf16 MFMA)
-//   P  = lower(q_i.k_j e^(gamma_i - gamma_j))                  (qk^T, bf16 MFMA)
-//   T  = (I + A)^-1 diag(beta)                                 (fp32 block substitution)
-//   R  = V - diag(e^gamma) K S                                 (split-bf16 MFMA)
-//   V' = T R                       (= u - w S of the reference, split-bf16 MFMA)
-//   O  = scale [diag(e^gamma) Q S + P V']                      (bf16 MFMA)
-//   S  = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'        (split-bf16 MFMA)
-// The MFMAs run in fp16 (v_mfma_f32_32x32x16_f16, same rate as bf16): q and
-// k are L2-normalised bf16 values, which fp16 holds exactly, and every fp32
-// operand that feeds the carried state (S, R, the decayed V', and T) is split
-// into fp16 hi + lo parts (22 mantissa bits).  Split operands are first
-// scaled by a per-wave power of two (max |x| in [2^9, 2^10)) so fp16 can
-// neither overflow nor flush them; the scale is undone on the fp32
-// accumulator.  Products that only feed o use the hi part alone.
+//   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kk^T, MFMA)
+//   P  = lower(q_i.k_j e^(gamma_i - gamma_j))                  (qk^T, MFMA)
+//   T  = (I + A)^-1 diag(beta)     (16x16 diagonal blocks by substitution,
+//                                   off-diagonal blocks by MFMA block merges)
+//   R  = V - diag(e^gamma) K S
+//   V' = T R                       (= u - w S of the reference)
+//   O  = scale [diag(e^gamma) Q S + P V']
+//   S  = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
 //
-// MFMA: v_mfma_f32_32x32x16_f16.  Operand layouts (lane l, n = l % 32,
-// g = l / 32): A[m][k] lane holds row n, 8 k; B[k][n] lane holds column n,
-// 8 k; C lane holds column n, rows 8i + 4g + r (i, r < 4).  A C-layout tile
-// whose rows are the contraction index is fed back as a B operand without
-// any data movement by ordering the 16-wide k-step as
-//   k = 16s + 8*(m / 4) + 4g + (m % 4),  m = 0..7 the operand slot,
-// and every A operand is read from LDS in that same order.
+// The MFMAs run in fp16 (same rate as bf16): q and k are L2-normalised bf16
+// values, which fp16 holds exactly, and every fp32 operand that feeds the
+// carried state (S, R, the decayed V', T and the merge operands) is split
+// into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  Split
+// operands are first scaled by a per-wave power of two (max |x| in
+// [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
+// undone on the fp32 accumulator.  Products that only feed o use the hi part.
+//
+// MFMA operand layouts (lane l, n = l % 32, g = l / 32), 32x32x16:
+// A[m][k] lane holds row n, 8 k; B[k][n] lane holds column n, 8 k; C lane
+// holds column n, rows 8i + 4g + r (i, r < 4).  A C-layout tile whose rows
+// are the contraction index is fed back as a B operand without data movement
+// by ordering each 16-wide k-step as k = 16s + 8*(m / 4) + 4g + (m % 4)
+// (m = operand slot), and every A operand is read from LDS in that order.
+// 16x16x16: A lane holds row l%16, k = 4(l/16)..+3; B column l%16, same k;
+// C column l%16, rows 4(l/16)..+3 (already in B order).
 #include "gdn_common.h"
 
 namespace {
@@ -41,9 +44,11 @@ constexpr int kThreads = 256;
 constexpr int C = 64;      // chunk
 constexpr int KD = 128;    // key head dim
 constexpr int VD = 128;    // value head dim
-constexpr int LDK = 152;   // bf16 row stride of the K/Q/V tiles (conflict-free b64 and transposed reads)
-constexpr int LDT = 72;    // bf16 row stride of T_hi/T_lo/P
+constexpr int LDK = 136;   // fp16 row stride of the K/Q tiles
+constexpr int LDV = 144;   // bf16 row stride of the V tile (conflict-free transposed reads)
 constexpr int LDA = 68;    // fp32 row stride of A/T
+constexpr int LDH = 68;    // fp16 row stride of T_hi/T_lo/P
+constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this many sequences
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -63,22 +68,31 @@ struct PrefillArgs {
 };
 
 struct Smem {
-  f16_t k[C * LDK];   // chunk keys (fp16)
-  f16_t q[C * LDK];   // chunk queries (fp16)
-  bf16_t v[C * LDK];  // chunk values; also the staging buffer of the chunk's output
-  float a[C * LDA];   // A, then T = (I + A)^-1 in place
-  float m[3][16 * 17];
-  f16_t thi[C * LDT];
-  f16_t tlo[C * LDT];
-  f16_t p[C * LDT];
+  f16_t k[C * LDK];
+  f16_t q[C * LDK];
+  bf16_t v[C * LDV];  // chunk values, then the staging buffer of the chunk's output
+  union {
+    float a[C * LDA];  // A, then T = (I + A)^-1 in place
+    struct {
+      f16_t hi[C * LDH];  // T' = T diag(beta), hi part
+      f16_t lo[C * LDH];  // lo part
+    } t;
+    int32_t lens[kMaxRankedSeqs];  // sequence lengths, before the first chunk
+  } u;
+  f16_t p[C * LDH];
   alignas(16) float gam[C];
   alignas(16) float eg[C];    // e^gamma
   alignas(16) float edec[C];  // e^(gamma_L - gamma), 0 past the chunk's last token
   alignas(16) float beta[C];
+  float gam_last;
+  int32_t seq;
 };
 
-GDN_DEVICE f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
+GDN_DEVICE f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+GDN_DEVICE f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
 GDN_DEVICE f32x16 zero16() {
@@ -92,34 +106,33 @@ GDN_DEVICE f16x8 cat4(f16x4 lo, f16x4 hi) {
   return (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Operand fragment of a row-major bf16 LDS matrix M: lane holds
-// M[r0 + n][k-step slots] -- an A operand (rows of M are the M dim) or a B
-// operand of M^T (rows of M are the N dim).
+// Fragment of a row-major fp16 LDS matrix M: lane holds M[r0 + n][k-step
+// slots] -- an A operand (rows of M are the M dim) or a B operand of M^T.
 GDN_DEVICE f16x8 frag_rows(const f16_t* M, int ld, int r0, int kbase, int lane) {
   const f16_t* p = M + (r0 + (lane & 31)) * ld + kbase + 4 * (lane >> 5);
   return cat4(*reinterpret_cast<const f16x4*>(p), *reinterpret_cast<const f16x4*>(p + 8));
 }
 
-// Operand fragment of the transpose of a row-major bf16 LDS matrix M: lane
-// holds M[k-step slots][c0 + n], read with the LDS transpose unit
-// (ds_read_b64_tr_b16: each 16-lane group reads a 4x16 block, lane i gets
-// column i).
+// Transposed read of a row-major 16-bit LDS matrix (ds_read_b64_tr_b16: each
+// 16-lane group reads a 4x16 block, lane i gets column i).
+GDN_DEVICE s16x4 tr_read(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+// Fragment of the transpose of a row-major fp16 LDS matrix M: lane holds
+// M[k-step slots][c0 + n].
 GDN_DEVICE f16x8 frag_cols(const f16_t* M, int ld, int c0, int kbase, int lane) {
   const int j = lane & 15, qd = lane >> 4;
   const f16_t* p = M + (kbase + 4 * (qd >> 1) + (j >> 2)) * ld + c0 + 16 * (qd & 1) + 4 * (j & 3);
-  s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * ld));
-  return cat4(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi));
+  return cat4(__builtin_bit_cast(f16x4, tr_read(p)), __builtin_bit_cast(f16x4, tr_read(p + 8 * ld)));
 }
 
-// Rows 8i + 4g + (0..3) of the C-layout tile starting at row r0 hold token
-// rows; fetch a per-row vector for them.
+// Per-row vector entries for C-layout rows r0 + 8i + 4g + (0..3).
 GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
 }
 
-// Power-of-two exponent e such that max|x| * 2^-e lies in [2^9, 2^10) over
-// the wave's `nt` C tiles (0 when all are zero); the same on every lane.
+// Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over the wave's
+// `nt` C tiles (0 when all are zero); the same on every lane.
 GDN_DEVICE int wave_scale_exp(const f32x16* t, int nt) {
   float m = 0.f;
   for (int i = 0; i < nt; ++i)
@@ -130,27 +143,171 @@ GDN_DEVICE int wave_scale_exp(const f32x16* t, int nt) {
   return m > 0.f ? __builtin_amdgcn_frexp_expf(m) - 10 : 0;
 }
 
-// hi/lo fp16 split of 8 fp32 values (registers 8h..8h+7 of a C tile) times sc
+// hi/lo fp16 splits: hi = fp16(x) (round to nearest even), lo = fp16(x - hi).
+// hi is converted once and its bits are pinned through an empty asm, so the
+// x - hi below is taken from exactly the bits that are stored as hi.  (If the
+// compiler is left to convert x twice it may pick the packed and the scalar
+// float->fp16 instructions for the two uses, and those can disagree on exact
+// rounding ties, which leaves lo referenced to a different hi.)
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+GDN_DEVICE void split_pair(float x0, float x1, f16_t& h0, f16_t& h1, f16_t& l0, f16_t& l1) {
+  const f32x2 x = {x0, x1};
+  uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
+  asm volatile("" : "+v"(hb));
+  const f16x2 h = __builtin_bit_cast(f16x2, hb);
+  const f32x2 r = {x0 - (float)h[0], x1 - (float)h[1]};
+  const f16x2 l = __builtin_convertvector(r, f16x2);
+  h0 = h[0];
+  h1 = h[1];
+  l0 = l[0];
+  l1 = l[1];
+}
+
+// split of registers 8h..8h+7 of a C tile, times sc
 GDN_DEVICE void split8(const f32x16& c, int h, float sc, f16x8& hi, f16x8& lo) {
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const float x = c[8 * h + m] * sc;
-    const f16_t xh = (f16_t)x;
-    hi[m] = xh;
-    lo[m] = (f16_t)(x - (float)xh);
+  for (int m = 0; m < 8; m += 2) {
+    f16_t a0, a1, b0, b1;
+    split_pair(c[8 * h + m] * sc, c[8 * h + m + 1] * sc, a0, a1, b0, b1);
+    hi[m] = a0;
+    hi[m + 1] = a1;
+    lo[m] = b0;
+    lo[m + 1] = b1;
   }
 }
-
-GDN_DEVICE f16x8 round8(const f32x16& c, int h, float sc) {
-  f16x8 r;
+template <int N>
+GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
+  static_assert(N % 2 == 0, "pairs");
 #pragma unroll
-  for (int m = 0; m < 8; ++m) r[m] = (f16_t)(c[8 * h + m] * sc);
-  return r;
+  for (int m = 0; m < N; m += 2) split_pair(x[m], x[m + 1], hi[m], hi[m + 1], lo[m], lo[m + 1]);
 }
 
-__global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
+// ---- T = (I + A)^-1 pieces (A strictly lower, fp32 in LDS) --------------------
+
+// Diagonal 16x16 blocks by right-looking forward substitution; lane (b, c)
+// = (lane / 16, lane % 16) computes column c of block b.  One wave.
+GDN_DEVICE void invert_diag_blocks(float* A, int lane) {
+  const int b = lane >> 4, c = lane & 15;
+  float* Ab = A + 16 * b * LDA + 16 * b;
+  float y[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) y[i] = i == c ? 1.f : 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 15; ++kk) {
+    const float xk = y[kk];
+#pragma unroll
+    for (int i = kk + 1; i < 16; ++i) y[i] = fmaf(-Ab[i * LDA + kk], xk, y[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) Ab[i * LDA + c] = y[i];
+}
+
+GDN_DEVICE void split4(f32x4 x, f16x4& hi, f16x4& lo) {
+  float xs[4] = {x[0], x[1], x[2], x[3]};
+  f16_t h[4], l[4];
+  split_vec<4>(xs, h, l);
+  hi = (f16x4){h[0], h[1], h[2], h[3]};
+  lo = (f16x4){l[0], l[1], l[2], l[3]};
+}
+
+// 16 -> 32 merge: T_10 = -T_11 A_10 T_00 for the 32-block starting at row and
+// column o (0 or 32), with 16x16x16 MFMAs on hi/lo splits.  One wave.
+GDN_DEVICE void merge16(float* A, int o, int lane) {
+  const int n = lane & 15, g4 = 4 * (lane >> 4);
+  f16x4 ah, al, bh, bl;
+  // M = A_10 T_00: A operand = rows of A_10, B operand = columns of T_00
+  split4(*reinterpret_cast<const f32x4*>(A + (o + 16 + n) * LDA + o + g4), ah, al);
+  {
+    f32x4 y;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) y[m] = A[(o + g4 + m) * LDA + o + n];
+    split4(y, bh, bl);
+  }
+  f32x4 M = {0.f, 0.f, 0.f, 0.f};
+  M = mfma16(ah, bh, M);
+  M = mfma16(ah, bl, M);
+  M = mfma16(al, bh, M);
+  // T_10 = -T_11 M: A operand = rows of T_11, B operand = M (C layout rows == k)
+  split4(*reinterpret_cast<const f32x4*>(A + (o + 16 + n) * LDA + o + 16 + g4), ah, al);
+  split4(M, bh, bl);
+  f32x4 R = {0.f, 0.f, 0.f, 0.f};
+  R = mfma16(ah, bh, R);
+  R = mfma16(ah, bl, R);
+  R = mfma16(al, bh, R);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) A[(o + 16 + g4 + m) * LDA + o + n] = -R[m];
+}
+
+// 32 -> 64 merge: T_10 = -T_11 A_10 T_00 with 32x32 blocks, 32x32x16 MFMAs on
+// hi/lo splits.  One wave.
+GDN_DEVICE void merge32(float* A, int lane) {
+  const int n = lane & 31, g4 = 4 * (lane >> 5);
+  f32x16 M = zero16();
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    // A operand: A_10[n][16ks + slots] = A[32 + n][...]; B operand: T_00[16ks + slots][n]
+    const float* pa = A + (32 + n) * LDA + 16 * ks + g4;
+    f16x4 ah0, al0, ah1, al1, bh0, bl0, bh1, bl1;
+    split4(*reinterpret_cast<const f32x4*>(pa), ah0, al0);
+    split4(*reinterpret_cast<const f32x4*>(pa + 8), ah1, al1);
+    f32x4 y0, y1;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      y0[m] = A[(16 * ks + g4 + m) * LDA + n];
+      y1[m] = A[(16 * ks + 8 + g4 + m) * LDA + n];
+    }
+    split4(y0, bh0, bl0);
+    split4(y1, bh1, bl1);
+    const f16x8 ah = cat4(ah0, ah1), al = cat4(al0, al1), bh = cat4(bh0, bh1), bl = cat4(bl0, bl1);
+    M = mfma32(ah, bh, M);
+    M = mfma32(ah, bl, M);
+    M = mfma32(al, bh, M);
+  }
+  f32x16 R = zero16();
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const float* pa = A + (32 + n) * LDA + 32 + 16 * ks + g4;
+    f16x4 ah0, al0, ah1, al1;
+    split4(*reinterpret_cast<const f32x4*>(pa), ah0, al0);
+    split4(*reinterpret_cast<const f32x4*>(pa + 8), ah1, al1);
+    f16x8 bh, bl;
+    split8(M, ks, 1.f, bh, bl);
+    const f16x8 ah = cat4(ah0, ah1), al = cat4(al0, al1);
+    R = mfma32(ah, bh, R);
+    R = mfma32(ah, bl, R);
+    R = mfma32(al, bh, R);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) A[(32 + 8 * (j >> 2) + g4 + (j & 3)) * LDA + n] = -R[j];
+}
+
+// Sequence of rank `rank` in longest-first order (ties by index); called by
+// every thread of the block.
+GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int tid) {
+  if (a.nseq > kMaxRankedSeqs) return rank;
+  for (int64_t i = tid; i < a.nseq; i += kThreads) {
+    int64_t s, e;
+    seq_range(a.cu, a.cu64, i, a.T, s, e);
+    sm.u.lens[i] = (int32_t)(e - s);
+  }
+  if (tid == 0) sm.seq = (int32_t)rank;
+  __syncthreads();
+  if (tid < a.nseq) {
+    const int32_t li = sm.u.lens[tid];
+    int64_t rk = 0;
+    for (int j = 0; j < a.nseq; ++j) {
+      const int32_t lj = sm.u.lens[j];
+      rk += (lj > li) || (lj == li && j < tid);
+    }
+    if (rk == rank) sm.seq = tid;
+  }
+  __syncthreads();
+  return sm.seq;
+}
+
+__global__ __launch_bounds__(kThreads)
+void gdn_chunk_prefill_kernel(PrefillArgs a) {
   __shared__ Smem sm;
-  __shared__ float gam_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -158,8 +315,13 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   const int n = lane & 31;
   const int gq = lane >> 5;
 
-  const int64_t seq = blockIdx.x / a.Hv;
-  const int h = blockIdx.x % a.Hv;
+  // Work id: consecutive v-heads (sharing a k-head) go to one XCD (workgroups
+  // are dealt round-robin over the 8 XCDs), sequences longest first.
+  const int64_t bid = blockIdx.x;
+  const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
+  if (work >= a.nseq * a.Hv) return;
+  const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
+  const int h = (int)(work % a.Hv);
   const int kh = h / a.r;
   int64_t s, e;
   seq_range(a.cu, a.cu64, seq, a.T, s, e);
@@ -188,40 +350,55 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   const bf16_t* kg = a.k + kh * a.k_s1;
   const bf16_t* vg = a.v + h * a.v_s1;
 
-  for (int64_t c0 = s; c0 < e; c0 += C) {
-    const int L = (int)((e - c0) < C ? (e - c0) : C);
-    __syncthreads();  // previous chunk is done with every LDS buffer
-
-    // ---- load the chunk's K, Q (k-head, to fp16) and V (v-head) tiles; zero rows past L
+  // the next chunk's inputs, prefetched into registers
+  bf16x8 pk[4], pq[4], pv[4];
+  float pgv = 0.f, pbv = 0.f;
+  auto prefetch = [&](int64_t c0) {
+    const int64_t rem = e - c0;
+    const int Lc = (int)(rem < C ? rem : C);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int vec = tid + u * kThreads;
       const int row = vec >> 4, cg = vec & 15;
-      bf16x8 kv, qv, vv;
-      if (row < L) {
+      if (row < Lc) {
         const int64_t t = c0 + row;
-        kv = *reinterpret_cast<const bf16x8*>(kg + t * a.k_s0 + 8 * cg);
-        qv = *reinterpret_cast<const bf16x8*>(qg + t * a.q_s0 + 8 * cg);
-        vv = *reinterpret_cast<const bf16x8*>(vg + t * a.v_s0 + 8 * cg);
+        pk[u] = *reinterpret_cast<const bf16x8*>(kg + t * a.k_s0 + 8 * cg);
+        pq[u] = *reinterpret_cast<const bf16x8*>(qg + t * a.q_s0 + 8 * cg);
+        pv[u] = *reinterpret_cast<const bf16x8*>(vg + t * a.v_s0 + 8 * cg);
       } else {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) { kv[m] = (bf16_t)0.f; qv[m] = (bf16_t)0.f; vv[m] = (bf16_t)0.f; }
+        for (int m = 0; m < 8; ++m) { pk[u][m] = (bf16_t)0.f; pq[u][m] = (bf16_t)0.f; pv[u][m] = (bf16_t)0.f; }
       }
-      f16x8 kh16, qh16;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) { kh16[m] = (f16_t)(float)kv[m]; qh16[m] = (f16_t)(float)qv[m]; }
-      *reinterpret_cast<f16x8*>(sm.k + row * LDK + 8 * cg) = kh16;
-      *reinterpret_cast<f16x8*>(sm.q + row * LDK + 8 * cg) = qh16;
-      *reinterpret_cast<bf16x8*>(sm.v + row * LDK + 8 * cg) = vv;
     }
-    // ---- gamma = in-chunk cumsum of g; decay vectors (wave 0, one token per lane)
     if (wave == 0) {
-      float gv = 0.f, bv = 0.f;
-      if (lane < L) {
-        gv = a.g[(c0 + lane) * a.g_s0 + h * a.g_s1];
-        bv = load_scalar_f32(a.beta, (c0 + lane) * a.b_s0 + h * a.b_s1, a.b_dtype);
+      pgv = 0.f;
+      pbv = 0.f;
+      if (lane < Lc) {
+        pgv = a.g[(c0 + lane) * a.g_s0 + h * a.g_s1];
+        pbv = load_scalar_f32(a.beta, (c0 + lane) * a.b_s0 + h * a.b_s1, a.b_dtype);
       }
-      float gm = gv;
+    }
+  };
+  prefetch(s);
+
+  for (int64_t c0 = s; c0 < e; c0 += C) {
+    const int L = (int)((e - c0) < C ? (e - c0) : C);
+    __syncthreads();  // every LDS buffer of the previous chunk is free
+
+    // ---- stage the chunk: K, Q to fp16, V as is; gamma = in-chunk cumsum of g (wave 0)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vec = tid + u * kThreads;
+      const int row = vec >> 4, cg = vec & 15;
+      f16x8 k16, q16;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) { k16[m] = (f16_t)(float)pk[u][m]; q16[m] = (f16_t)(float)pq[u][m]; }
+      *reinterpret_cast<f16x8*>(sm.k + row * LDK + 8 * cg) = k16;
+      *reinterpret_cast<f16x8*>(sm.q + row * LDK + 8 * cg) = q16;
+      *reinterpret_cast<bf16x8*>(sm.v + row * LDV + 8 * cg) = pv[u];
+    }
+    if (wave == 0) {
+      float gm = pgv;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float y = __shfl_up(gm, off, 64);
@@ -231,170 +408,168 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       sm.gam[lane] = gm;
       sm.eg[lane] = __expf(gm);
       sm.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
-      sm.beta[lane] = bv;
-      if (lane == 0) gam_last = gl;
+      sm.beta[lane] = pbv;
+      if (lane == 0) sm.gam_last = gl;
     }
     __syncthreads();
 
-    // ---- A = strict_lower(beta_i G_ij e^(g_i - g_j)) and P = lower(QK^T e^(g_i - g_j))
+    // ---- A = strict_lower(beta_i (K K^T)_ij e^(g_i - g_j)): 32x32 tiles (0,0), (1,0), (1,1)
     if (wave < 3) {
       const int mt = wave == 0 ? 0 : 1;
       const int nt = wave == 2 ? 1 : 0;
-      f32x16 G = zero16(), Pq = zero16();
+      f32x16 G = zero16();
 #pragma unroll
-      for (int ks = 0; ks < KD / 16; ++ks) {
-        const f16x8 bk = frag_rows(sm.k, LDK, 32 * nt, 16 * ks, lane);
-        G = mfma(frag_rows(sm.k, LDK, 32 * mt, 16 * ks, lane), bk, G);
-        Pq = mfma(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), bk, Pq);
-      }
+      for (int ks = 0; ks < KD / 16; ++ks)
+        G = mfma32(frag_rows(sm.k, LDK, 32 * mt, 16 * ks, lane), frag_rows(sm.k, LDK, 32 * nt, 16 * ks, lane), G);
       const int j = 32 * nt + n;
       const float gj = sm.gam[j];
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int i = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
-        const float dec = i >= j ? __expf(sm.gam[i] - gj) : 0.f;
-        sm.a[i * LDA + j] = i > j ? sm.beta[i] * G[jj] * dec : 0.f;
-        sm.p[i * LDT + j] = (f16_t)(Pq[jj] * dec);
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 gi = rows4(sm.gam, 32 * mt, i4, lane);
+        const f32x4 bi = rows4(sm.beta, 32 * mt, i4, lane);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+          sm.u.a[i * LDA + j] = i > j ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+        }
       }
-    } else {  // upper 32x32 tiles are zero
+    } else {  // upper 32x32 tile of A and P are zero
       for (int x = lane; x < 32 * 32; x += 64) {
         const int i = x >> 5, j = 32 + (x & 31);
-        sm.a[i * LDA + j] = 0.f;
-        sm.p[i * LDT + j] = (f16_t)0.f;
+        sm.u.a[i * LDA + j] = 0.f;
+        sm.p[i * LDH + j] = (f16_t)0.f;
       }
     }
     __syncthreads();
 
-    // ---- T = (I + A)^-1: 16x16 diagonal blocks by forward substitution
+    // ---- wave 0: diagonal blocks of T; waves 1-3: P = lower(Q K^T e^(g_i - g_j))
     if (wave == 0) {
-      const int b = lane >> 4, c = lane & 15;
-      const float* Ab = sm.a + 16 * b * LDA + 16 * b;
-      float x[16];
+      invert_diag_blocks(sm.u.a, lane);
+    } else {
+      const int mt = wave == 1 ? 0 : 1;
+      const int nt = wave == 3 ? 1 : 0;
+      f32x16 Pq = zero16();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float acc = 0.f;
+      for (int ks = 0; ks < KD / 16; ++ks)
+        Pq = mfma32(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), frag_rows(sm.k, LDK, 32 * nt, 16 * ks, lane), Pq);
+      const int j = 32 * nt + n;
+      const float gj = sm.gam[j];
 #pragma unroll
-        for (int kk = 0; kk < i; ++kk) acc = fmaf(Ab[i * LDA + kk], x[kk], acc);
-        x[i] = i == c ? 1.f : (i < c ? 0.f : -acc);
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 gi = rows4(sm.gam, 32 * mt, i4, lane);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+          sm.p[i * LDH + j] = (f16_t)(i >= j ? Pq[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sm.a[(16 * b + i) * LDA + 16 * b + c] = x[i];
     }
     __syncthreads();
-    // off-diagonal blocks, one block row at a time:
-    //   T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj
+    if (wave < 2) merge16(sm.u.a, 32 * wave, lane);
+    __syncthreads();
+    if (wave == 0) merge32(sm.u.a, lane);
+    __syncthreads();
+    // ---- T' = T diag(beta) as fp16 hi/lo, in place over the fp32 T
     {
-      const int rr = tid >> 4, cc = tid & 15;
+      float tv[16];
+      const int i = tid >> 2, j0 = 16 * (tid & 3);
 #pragma unroll
-      for (int bi = 1; bi < 4; ++bi) {
-        for (int bj = 0; bj < bi; ++bj) {
-          float acc = 0.f;
-          for (int bk = bj; bk < bi; ++bk) {
-            const float* Ar = sm.a + (16 * bi + rr) * LDA + 16 * bk;
-            const float* Tc = sm.a + (16 * bk) * LDA + 16 * bj + cc;
+      for (int m = 0; m < 16; m += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(sm.u.a + i * LDA + j0 + m);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(sm.beta + j0 + m);
 #pragma unroll
-            for (int x = 0; x < 16; ++x) acc = fmaf(Ar[x], Tc[x * LDA], acc);
-          }
-          sm.m[bj][rr * 17 + cc] = acc;
-        }
-        __syncthreads();
-        for (int bj = 0; bj < bi; ++bj) {
-          const float* Tr = sm.a + (16 * bi + rr) * LDA + 16 * bi;
-          float acc = 0.f;
+        for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
+      }
+      f16_t th[16], tl[16];
+      split_vec<16>(tv, th, tl);
+      __syncthreads();
 #pragma unroll
-          for (int x = 0; x < 16; ++x) acc = fmaf(Tr[x], sm.m[bj][x * 17 + cc], acc);
-          sm.a[(16 * bi + rr) * LDA + 16 * bj + cc] = -acc;
-        }
-        __syncthreads();
+      for (int m = 0; m < 16; m += 4) {
+        *reinterpret_cast<f16x4*>(sm.u.t.hi + i * LDH + j0 + m) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
+        *reinterpret_cast<f16x4*>(sm.u.t.lo + i * LDH + j0 + m) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
       }
     }
-    // ---- T' = T diag(beta) as hi/lo fp16
-    for (int x = tid; x < C * C; x += kThreads) {
-      const int i = x >> 6, j = x & 63;
-      const float t = sm.a[i * LDA + j] * sm.beta[j];
-      const f16_t th = (f16_t)t;
-      sm.thi[i * LDT + j] = th;
-      sm.tlo[i * LDT + j] = (f16_t)(t - (float)th);
-    }
     __syncthreads();
+
+    if (c0 + C < e) prefetch(c0 + C);
 
     // ---- per-wave state products on this wave's 32 value columns
     const int es = wave_scale_exp(S, 4);
     const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
-    f16x8 shi[8], slo[8];
+    f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) split8(S[ks >> 1], ks & 1, ss, shi[ks], slo[ks]);
-
-    f32x16 X[2], QS[2];
+    for (int ks = 0; ks < 8; ++ks) {
+      f16x8 shi, slo;
+      split8(S[ks >> 1], ks & 1, ss, shi, slo);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      X[mt] = zero16();
-      QS[mt] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+      for (int mt = 0; mt < 2; ++mt) {
         const f16x8 ak = frag_rows(sm.k, LDK, 32 * mt, 16 * ks, lane);
-        X[mt] = mfma(ak, shi[ks], X[mt]);
-        X[mt] = mfma(ak, slo[ks], X[mt]);
-        QS[mt] = mfma(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), shi[ks], QS[mt]);
+        X[mt] = mfma32(ak, shi, X[mt]);
+        X[mt] = mfma32(ak, slo, X[mt]);
+        QS[mt] = mfma32(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), shi, QS[mt]);
       }
     }
-    // R = V - diag(e^gamma) X  (X, QS are in units of 2^-es; V read transposed: rows are tokens)
+    // R = V - diag(e^gamma) X (X, QS in units of 2^-es; V read transposed: rows are tokens)
     const float us = __builtin_amdgcn_ldexpf(1.f, es);
-    f32x16 R[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 egv = rows4(sm.eg, 32 * mt, i, lane);
         const int j = lane & 15, qd = lane >> 4;
-        const bf16_t* p = sm.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDK + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
-        const bf16x4 vv = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+        const bf16_t* p = sm.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
+        const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) R[mt][4 * i + rr] = (float)vv[rr] - egv[rr] * (X[mt][4 * i + rr] * us);
+        for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = (float)vv[rr] - egv[rr] * (X[mt][4 * i + rr] * us);
       }
     }
+    f32x16* R = X;  // X now holds R
     const int er = wave_scale_exp(R, 2);
     const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
-    f16x8 rhi[4], rlo[4];
+    // V' = T' R, in units of 2^-er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
+    f32x16 VN[2] = {zero16(), zero16()};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) split8(R[ks >> 1], ks & 1, rs, rhi[ks], rlo[ks]);
-    // V' = T' R, in units of 2^-er (T' lower triangular: the first 32 rows need only k-steps 0, 1)
-    f32x16 VN[2];
+    for (int ks = 0; ks < 4; ++ks) {
+      f16x8 rhi, rlo;
+      split8(R[ks >> 1], ks & 1, rs, rhi, rlo);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      VN[mt] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 2 * (mt + 1); ++ks) {
-        const f16x8 ah = frag_rows(sm.thi, LDT, 32 * mt, 16 * ks, lane);
-        const f16x8 al = frag_rows(sm.tlo, LDT, 32 * mt, 16 * ks, lane);
-        VN[mt] = mfma(ah, rhi[ks], VN[mt]);
-        VN[mt] = mfma(ah, rlo[ks], VN[mt]);
-        VN[mt] = mfma(al, rhi[ks], VN[mt]);
+      for (int mt = (ks >> 1); mt < 2; ++mt) {
+        const f16x8 ah = frag_rows(sm.u.t.hi, LDH, 32 * mt, 16 * ks, lane);
+        const f16x8 al = frag_rows(sm.u.t.lo, LDH, 32 * mt, 16 * ks, lane);
+        VN[mt] = mfma32(ah, rhi, VN[mt]);
+        VN[mt] = mfma32(ah, rlo, VN[mt]);
+        VN[mt] = mfma32(al, rhi, VN[mt]);
       }
     }
     // O = scale (diag(e^gamma) Q S + P V'), staged as bf16 in this wave's columns of sm.v
-    f16x8 vnb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) vnb[ks] = round8(VN[ks >> 1], ks & 1, 1.f);
     const float ru = __builtin_amdgcn_ldexpf(1.f, er);
     const float qsu = __builtin_amdgcn_ldexpf(1.f, es - er);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      f32x16 O;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 egv = rows4(sm.eg, 32 * mt, i, lane);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) O[4 * i + rr] = egv[rr] * QS[mt][4 * i + rr] * qsu;
+        for (int rr = 0; rr < 4; ++rr) QS[mt][4 * i + rr] *= egv[rr] * qsu;
       }
+    }
 #pragma unroll
-      for (int ks = 0; ks < 2 * (mt + 1); ++ks) O = mfma(frag_rows(sm.p, LDT, 32 * mt, 16 * ks, lane), vnb[ks], O);
+    for (int ks = 0; ks < 4; ++ks) {
+      f16x8 vb;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) vb[m] = (f16_t)VN[ks >> 1][8 * (ks & 1) + m];
+#pragma unroll
+      for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(sm.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
+    }
+    {
       const float osc = ru * a.scale;
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
-        sm.v[row * LDK + col] = (bf16_t)(O[jj] * osc);
-      }
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
+          sm.v[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
+        }
     }
     // S = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
 #pragma unroll
@@ -408,26 +583,28 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     }
     const int ed = wave_scale_exp(VN, 2);
     const float ds = __builtin_amdgcn_ldexpf(1.f, -ed);
-    f16x8 dhi[4], dlo[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) split8(VN[ks >> 1], ks & 1, ds, dhi[ks], dlo[ks]);
-    // accumulate in units of 2^(er + ed): S_acc = S * 2^-(er+ed) + K^T Vd_scaled
-    const float egl = __expf(gam_last);
-    const float sin_ = egl * __builtin_amdgcn_ldexpf(1.f, -(er + ed));
+    // accumulate in units of 2^-(er + ed): S_acc = e^gamma_L S 2^-(er+ed) + K^T Vd_scaled
+    const float sin_ = __expf(sm.gam_last) * __builtin_amdgcn_ldexpf(1.f, -(er + ed));
     const float sout = __builtin_amdgcn_ldexpf(1.f, er + ed);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] *= sin_;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < 4; ++ks) {
+      f16x8 dhi, dlo;
+      split8(VN[ks >> 1], ks & 1, ds, dhi, dlo);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
         const f16x8 akt = frag_cols(sm.k, LDK, 32 * mt, 16 * ks, lane);
-        S[mt] = mfma(akt, dhi[ks], S[mt]);
-        S[mt] = mfma(akt, dlo[ks], S[mt]);
+        S[mt] = mfma32(akt, dhi, S[mt]);
+        S[mt] = mfma32(akt, dlo, S[mt]);
       }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] *= sout;
-    }
     __syncthreads();
     // ---- store the chunk's output rows
 #pragma unroll
@@ -436,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       const int row = vec >> 4, cg = vec & 15;
       if (row < L)
         *reinterpret_cast<bf16x8*>(a.out + (c0 + row) * a.o_s0 + h * a.o_s1 + 8 * cg) =
-            *reinterpret_cast<const bf16x8*>(sm.v + row * LDK + 8 * cg);
+            *reinterpret_cast<const bf16x8*>(sm.v + row * LDV + 8 * cg);
     }
   }
 
@@ -479,8 +656,9 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   a.scale = scale;
   a.idx64 = idx->dtype == GDN_DTYPE_I64;
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
-  const int64_t nblocks = a.nseq * a.Hv;
-  if (nblocks == 0 || a.T == 0) return hipSuccess;
+  const int64_t nwork = a.nseq * a.Hv;
+  if (nwork == 0 || a.T == 0) return hipSuccess;
+  const int64_t nblocks = (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
   gdn_chunk_prefill_kernel<<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
   return hipGetLastError();
 }
