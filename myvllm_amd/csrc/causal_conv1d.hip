@@ -8,11 +8,11 @@
 // the W-1 previous inputs in registers, so x is read once (plus a W-1 row
 // halo per 64-token tile) and y written once, fully coalesced.
 //
-// Prefill tiling: each sequence is cut into 64-token tiles; blockIdx.x is a
+// Prefill tiling: each sequence is cut into 32-token tiles; blockIdx.x is a
 // linear tile id resolved to (sequence, tile) on the device, so no host sync
 // is needed (the reference calls .tolist() on cu_seqlens, ops/causal_conv1d.py:230).
 // Only a sequence's first tile reads its old conv state (a later tile's
-// window starts >= 64 > W-1 tokens into the sequence), and that same tile
+// window starts >= 32 > W-1 tokens into the sequence), and that same tile
 // writes the new state, so the read-before-write order on a slot is the
 // program order of one thread.
 #include "gdn_common.h"
@@ -20,7 +20,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTile = 64;  // tokens per prefill tile
+constexpr int kTile = 32;  // tokens per prefill tile (>= W - 1, see the state-ownership note)
 constexpr int kCh = 8;     // channels per thread
 constexpr int kBatch = 8;  // token rows loaded together
 
@@ -78,26 +78,24 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
       Vec8<TS>::load(st + (p - s + W - 1) * a.st_s1, win[m]);
     }
   }
-  float old_state[W - 1][kCh];
-  if (tile == 0) {
-#pragma unroll
-    for (int m = 0; m < W - 1; ++m)
-#pragma unroll
-      for (int c = 0; c < kCh; ++c) old_state[m][c] = win[m][c];
-  }
 
-  for (int64_t tb = t0; tb < t1; tb += kBatch) {
-    float xr[kBatch][kCh];
+  // token rows in batches of kBatch, the next batch's loads in flight while
+  // the current one is computed (two statically named buffers)
+  Raw8<TX> xa[kBatch], xb[kBatch];
+  auto load_batch = [&](int64_t tb, Raw8<TX>* dst) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (tb + u < t1) Vec8<TX>::load(x + (tb + u) * a.x_s0 + d0, xr[u]);
+      if (tb + u < t1) dst[u].load(x + (tb + u) * a.x_s0 + d0);
+  };
+  auto run_batch = [&](int64_t tb, const Raw8<TX>* raw) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (tb + u < t1) {
-        float y[kCh];
+        float xr[kCh], y[kCh];
+        raw[u].expand(xr);
 #pragma unroll
         for (int c = 0; c < kCh; ++c) {
-          float acc = wr[W - 1][c] * xr[u][c];
+          float acc = wr[W - 1][c] * xr[c];
 #pragma unroll
           for (int m = 0; m < W - 1; ++m) acc = fmaf(wr[m][c], win[m][c], acc);
           y[c] = silu_f32(acc);
@@ -108,9 +106,17 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
 #pragma unroll
           for (int c = 0; c < kCh; ++c) win[m][c] = win[m + 1][c];
 #pragma unroll
-        for (int c = 0; c < kCh; ++c) win[W - 2][c] = xr[u][c];
+        for (int c = 0; c < kCh; ++c) win[W - 2][c] = xr[c];
       }
     }
+  };
+  load_batch(t0, xa);
+  for (int64_t tb = t0; tb < t1; tb += 2 * kBatch) {
+    if (tb + kBatch < t1) load_batch(tb + kBatch, xb);
+    run_batch(tb, xa);
+    if (tb + kBatch >= t1) break;
+    if (tb + 2 * kBatch < t1) load_batch(tb + 2 * kBatch, xa);
+    run_batch(tb + kBatch, xb);
   }
 
   if (tile == 0) {  // new state = last W-1 rows of [old state; x_seq]
@@ -120,9 +126,8 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
       float row[kCh];
       if (p >= s) {
         Vec8<TX>::load(x + p * a.x_s0 + d0, row);
-      } else {
-#pragma unroll
-        for (int c = 0; c < kCh; ++c) row[c] = old_state[p - s + W - 1][c];
+      } else {  // old row p - s + W - 1 > r: not yet overwritten (rows are written in increasing order)
+        Vec8<TS>::load(st + (p - s + W - 1) * a.st_s1, row);
       }
       Vec8<TS>::store(st + r * a.st_s1, row);
     }

@@ -74,6 +74,38 @@ template <> struct Vec8<float> {
   }
 };
 
+// 8 consecutive elements kept in their storage type (fewer registers than
+// fp32 while a batch of rows is in flight); expand() widens to fp32.
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16_t> {
+  bf16x8 v;
+  GDN_DEVICE void load(const bf16_t* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  GDN_DEVICE void expand(float* f) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+  }
+};
+template <> struct Raw8<f16_t> {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  h8 v;
+  GDN_DEVICE void load(const f16_t* p) { v = *reinterpret_cast<const h8*>(p); }
+  GDN_DEVICE void expand(float* f) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+  }
+};
+template <> struct Raw8<float> {
+  f32x4 a, b;
+  GDN_DEVICE void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  GDN_DEVICE void expand(float* f) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
+  }
+};
+
 // Scalar of a runtime-typed float tensor (used for per-row scalars like g, beta).
 GDN_DEVICE float load_scalar_f32(const void* p, int64_t off, int dtype) {
   switch (dtype) {

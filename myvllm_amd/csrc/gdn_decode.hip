@@ -7,7 +7,8 @@
 // (sequence, v-head): every thread streams V/4-wide rows with 16-byte loads
 // (a wave reads 1 KiB contiguous per instruction), both reductions over K
 // (k^T S and q^T S) are done in the same pass, and the updated state is
-// written back in place, so the state crosses HBM exactly once each way.
+// written back in place, so the state crosses HBM exactly once each way
+// (non-temporal loads and stores: nothing of it is reused by this launch).
 //
 // Math per (b, h), with S decayed first (fused_recurrent_gdn.py:96-99):
 //   kS = k^T S, qS = (scale q)^T S                  (old S)
@@ -60,7 +61,8 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
   float* S = a.state + slot * a.st_slot + h * a.st_head;
   f32x4 s[NI];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) s[i] = *reinterpret_cast<const f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4);
+  for (int i = 0; i < NI; ++i)
+    s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4));
 
   if (tid < K) {
     sq[tid] = to_f32(reinterpret_cast<const TIn*>(a.q)[b * a.q_s0 + kh * a.q_s1 + tid]) * a.scale;
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
     f32x4 t;
 #pragma unroll
     for (int j = 0; j < 4; ++j) t[j] = fmaf(eg, s[i][j], kv * d[j]);
-    *reinterpret_cast<f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4) = t;
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4));
   }
   if (r0 == 0) {
 #pragma unroll

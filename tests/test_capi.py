@@ -1,0 +1,180 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol,
+and rejects malformed calls before launching anything.
+
+The validation calls use CPU tensors, so these tests are skipped where a GPU
+is visible (a validation bug there would hand host pointers to a kernel);
+the GPU tests cover the accepted paths.
+"""
+import os
+import re
+
+import pytest
+import torch
+
+from myvllm_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gdn_hip.h")
+
+ERR = {"NULL": -1, "NDIM": -2, "SHAPE": -3, "DTYPE": -4, "STRIDE": -5, "HEADS": -6, "HEAD_DIM": -7, "CHUNK": -8,
+       "ALIGN": -9, "CONV_WIDTH": -10, "RANGE": -11}
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|char\s*\*|size_t|void)\s*\*?\s*(\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_ffi_surface():
+    assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_error_codes_match():
+    text = open(HEADER).read()
+    for name, code in ERR.items():
+        assert re.search(rf"#define GDN_ERR_{name} \({code}\)", text), name
+    for code in list(ERR.values()) + [0]:
+        assert _lib.strerror(code) != "unknown error code"
+    assert _lib.strerror(-99) == "unknown error code"
+
+
+cpu_only = pytest.mark.skipif(torch.cuda.is_available(), reason="validation tests hand CPU pointers to the C ABI")
+
+D = _lib.describe
+
+
+def _recurrent_args(B=2, Hk=2, Hv=4, K=128, V=128, slots=3, dtype=torch.bfloat16):
+    return dict(
+        q=torch.zeros(B, Hk, K, dtype=dtype), k=torch.zeros(B, Hk, K, dtype=dtype), v=torch.zeros(B, Hv, V, dtype=dtype),
+        g=torch.zeros(B, Hv), beta=torch.zeros(B, Hv), state=torch.zeros(slots, Hv, K, V),
+        idx=torch.zeros(B, dtype=torch.int32), out=torch.zeros(B, Hv, V, dtype=dtype),
+    )
+
+
+def _call_recurrent(a):
+    lib = _lib.load()
+    return lib.gdn_recurrent_step(D(a["q"]), D(a["k"]), D(a["v"]), D(a["g"]), D(a["beta"]), D(a["state"]),
+                                  D(a["idx"]), D(a["out"]), 1.0, None)
+
+
+def _call_prefill(a, cu, chunk=64):
+    lib = _lib.load()
+    return lib.gdn_chunk_prefill(D(a["q"]), D(a["k"]), D(a["v"]), D(a["g"]), D(a["beta"]), D(a["state"]),
+                                 D(a["idx"]), D(cu), D(a["out"]), 1.0, chunk, None)
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "mutate, code",
+    [
+        (lambda a: a.update(g=torch.zeros(2, 4, 1)), "NDIM"),
+        (lambda a: a.update(v=torch.zeros(3, 4, 128, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(state=torch.zeros(3, 2, 128, 128)), "SHAPE"),
+        (lambda a: a.update(idx=torch.zeros(3, dtype=torch.int32)), "SHAPE"),
+        (lambda a: a.update(v=torch.zeros(2, 3, 128, dtype=torch.bfloat16), out=torch.zeros(2, 3, 128, dtype=torch.bfloat16),
+                            g=torch.zeros(2, 3), beta=torch.zeros(2, 3), state=torch.zeros(3, 3, 128, 128)), "HEADS"),
+        (lambda a: a.update(out=torch.zeros(2, 4, 128, dtype=torch.float32)), "DTYPE"),
+        (lambda a: a.update(state=torch.zeros(3, 4, 128, 128, dtype=torch.bfloat16)), "DTYPE"),
+        (lambda a: a.update(idx=torch.zeros(2, dtype=torch.float32)), "DTYPE"),
+        (lambda a: a.update(q=torch.zeros(2, 2, 256, dtype=torch.bfloat16)[:, :, ::2]), "STRIDE"),
+        (lambda a: a.update(state=torch.zeros(3, 4, 128, 256)[..., :128]), "STRIDE"),
+        (lambda a: a.update(**_recurrent_args(K=96, V=96)), "HEAD_DIM"),
+    ],
+)
+def test_recurrent_step_validation(mutate, code):
+    a = _recurrent_args()
+    mutate(a)
+    assert _call_recurrent(a) == ERR[code]
+
+
+@cpu_only
+def test_recurrent_step_null_descriptor():
+    a = _recurrent_args()
+    lib = _lib.load()
+    rc = lib.gdn_recurrent_step(None, D(a["k"]), D(a["v"]), D(a["g"]), D(a["beta"]), D(a["state"]), D(a["idx"]),
+                                D(a["out"]), 1.0, None)
+    assert rc == ERR["NULL"]
+
+
+@cpu_only
+def test_prefill_validation():
+    a = _recurrent_args(B=10)
+    a["idx"] = torch.zeros(2, dtype=torch.int32)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    assert _call_prefill(a, cu, chunk=32) == ERR["CHUNK"]
+    assert _call_prefill(a, torch.tensor([0, 10], dtype=torch.int32)) == ERR["SHAPE"]  # idx has 2 entries
+    b = _recurrent_args(B=10, dtype=torch.float32)
+    b["idx"] = torch.zeros(2, dtype=torch.int32)
+    assert _call_prefill(b, cu) == ERR["DTYPE"]  # prefill takes bf16 q/k/v only
+    c = _recurrent_args(B=10, K=64, V=64)
+    c["idx"] = torch.zeros(2, dtype=torch.int32)
+    assert _call_prefill(c, cu) == ERR["HEAD_DIM"]
+    d = _recurrent_args(B=10)
+    d["idx"] = torch.zeros(2, dtype=torch.int32)
+    d["g"] = torch.zeros(10, 4, dtype=torch.bfloat16)
+    assert _call_prefill(d, cu) == ERR["DTYPE"]
+    e = _recurrent_args(B=10)
+    e["idx"] = torch.zeros(2, dtype=torch.int32)
+    e["v"] = torch.zeros(10, 4, 130, dtype=torch.bfloat16)[:, :, 1:129]  # 2-byte offset: misaligned
+    assert _call_prefill(e, cu) == ERR["ALIGN"]
+
+
+def _conv_args(T=6, D_=64, W=4, slots=3, N=2):
+    return dict(x=torch.zeros(T, D_, dtype=torch.bfloat16), w=torch.zeros(D_, W, dtype=torch.bfloat16),
+                st=torch.zeros(slots, W - 1, D_), idx=torch.zeros(N, dtype=torch.int32),
+                cu=torch.tensor([0, 2, T], dtype=torch.int32), out=torch.zeros(T, D_, dtype=torch.bfloat16))
+
+
+def _call_conv(a):
+    return _lib.load().causal_conv1d_varlen(D(a["x"]), D(a["w"]), D(a["st"]), D(a["idx"]), D(a["cu"]), D(a["out"]),
+                                            None)
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "mutate, code",
+    [
+        (lambda a: a.update(w=torch.zeros(64, 7, dtype=torch.bfloat16), st=torch.zeros(3, 6, 64)), "CONV_WIDTH"),
+        (lambda a: a.update(w=torch.zeros(64, 1, dtype=torch.bfloat16), st=torch.zeros(3, 0, 64)), "CONV_WIDTH"),
+        (lambda a: a.update(st=torch.zeros(3, 2, 64)), "SHAPE"),
+        (lambda a: a.update(x=torch.zeros(6, 60, dtype=torch.bfloat16), w=torch.zeros(60, 4, dtype=torch.bfloat16),
+                            st=torch.zeros(3, 3, 60), out=torch.zeros(6, 60, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(out=torch.zeros(6, 64)), "DTYPE"),
+        (lambda a: a.update(w=torch.zeros(64, 4, dtype=torch.float16)), "DTYPE"),
+        (lambda a: a.update(cu=torch.zeros(3, dtype=torch.float32)), "DTYPE"),
+        (lambda a: a.update(x=torch.zeros(64, 6, dtype=torch.bfloat16).t()), "STRIDE"),
+        (lambda a: a.update(x=torch.zeros(6, 72, dtype=torch.bfloat16)[:, 4:68]), "ALIGN"),
+    ],
+)
+def test_conv_validation(mutate, code):
+    a = _conv_args()
+    mutate(a)
+    assert _call_conv(a) == ERR[code]
+
+
+@cpu_only
+def test_conv_step_validation():
+    lib = _lib.load()
+    x = torch.zeros(3, 64, dtype=torch.bfloat16)
+    rc = lib.causal_conv1d_step(D(x), D(torch.zeros(64, 4, dtype=torch.bfloat16)), D(torch.zeros(4, 3, 64)),
+                                D(torch.zeros(2, dtype=torch.int32)), D(torch.zeros(3, 64, dtype=torch.bfloat16)), None)
+    assert rc == ERR["SHAPE"]  # 3 tokens, 2 slot indices
+
+
+def test_ops_reject_cpu_tensors():
+    from myvllm_amd import causal_conv1d_update, recurrent_gated_delta_rule
+
+    a = _recurrent_args()
+    with pytest.raises(ValueError):
+        recurrent_gated_delta_rule(a["q"], a["k"], a["v"], a["g"], a["beta"], a["state"], a["idx"])
+    c = _conv_args()
+    with pytest.raises(ValueError):
+        causal_conv1d_update(c["x"][:2], c["w"], c["st"], c["idx"])
