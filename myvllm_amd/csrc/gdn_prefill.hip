@@ -3,12 +3,19 @@
 // Replaces the six-kernel Triton pipeline of chunk_gated_delta_rule
 // (ops/gated_delta_rule/gated_delta_rule.py:31-66 in yuyifanbupt/myvllm:
 // cumsum.py, chunk_scaled_dot_kkt.py, solve_tril.py, wu.py, h.py, o.py), which
-// round-trips A, w, u, the per-chunk states h and v_new through HBM.  Here a
-// 256-thread workgroup walks the chunks of one sequence for one v-head and
-// keeps everything on chip: the fp32 128x128 state lives in the registers of
-// its 4 waves (wave w owns value columns [32w, 32w+32)), the chunk's K/Q/V
-// tiles and the 64x64 chunk matrices live in LDS (< 80 KiB, so two
-// workgroups share a CU), and only q/k/v/g/beta are read and o written.
+// round-trips A, w, u, the per-chunk states h and v_new through HBM.  Here one
+// 512-thread workgroup walks the chunks of one sequence for one v-head and
+// keeps everything on chip; only q/k/v/g/beta are read and o written.
+//
+// The workgroup is split by role, and the two roles are software-pipelined
+// over chunks through a double-buffered LDS chunk slot (2 x 80 KiB):
+//  * state waves 0..3 hold the fp32 128x128 state in registers (wave w owns
+//    value columns [32w, 32w+32)) and run the state products of chunk c;
+//  * producer waves 4..7 stage chunk c+1 (K, Q, V, decays) into the other
+//    slot and compute everything that does not depend on the state: the
+//    kk^T and qk^T tiles, A, T = (I + A)^-1 diag(beta) and P.
+// Both roles execute one workgroup barrier per chunk; producers synchronise
+// among themselves through an LDS counter.
 //
 // Per chunk of L <= 64 tokens (gamma = in-chunk cumsum of g):
 //   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kk^T, MFMA)
@@ -40,7 +47,8 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;        // 4 state waves + 4 producer waves
+constexpr int kRoleThreads = 256;    // threads per role
 constexpr int C = 64;      // chunk
 constexpr int KD = 128;    // key head dim
 constexpr int VD = 128;    // value head dim
@@ -49,6 +57,7 @@ constexpr int LDV = 144;   // bf16 row stride of the V tile (conflict-free trans
 constexpr int LDA = 68;    // fp32 row stride of A/T
 constexpr int LDH = 68;    // fp16 row stride of T_hi/T_lo/P
 constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this many sequences
+constexpr int kSpinLimit = 1 << 22;  // bound on a producer barrier wait (never reached when correct)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -67,7 +76,8 @@ struct PrefillArgs {
   bool idx64, cu64;
 };
 
-struct Smem {
+// One chunk's on-chip data (80,400 bytes); the kernel holds two.
+struct ChunkSlot {
   f16_t k[C * LDK];
   f16_t q[C * LDK];
   bf16_t v[C * LDV];  // chunk values, then the staging buffer of the chunk's output
@@ -85,6 +95,11 @@ struct Smem {
   alignas(16) float edec[C];  // e^(gamma_L - gamma), 0 past the chunk's last token
   alignas(16) float beta[C];
   float gam_last;
+};
+
+struct Smem {
+  ChunkSlot slot[2];
+  int32_t producer_count;  // producer barrier arrivals
   int32_t seq;
 };
 
@@ -282,21 +297,22 @@ GDN_DEVICE void merge32(float* A, int lane) {
 }
 
 // Sequence of rank `rank` in longest-first order (ties by index); called by
-// every thread of the block.
+// every thread of the block (the lengths are staged in slot 1, unused yet).
 GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int tid) {
   if (a.nseq > kMaxRankedSeqs) return rank;
+  int32_t* lens = sm.slot[1].u.lens;
   for (int64_t i = tid; i < a.nseq; i += kThreads) {
     int64_t s, e;
     seq_range(a.cu, a.cu64, i, a.T, s, e);
-    sm.u.lens[i] = (int32_t)(e - s);
+    lens[i] = (int32_t)(e - s);
   }
   if (tid == 0) sm.seq = (int32_t)rank;
   __syncthreads();
   if (tid < a.nseq) {
-    const int32_t li = sm.u.lens[tid];
+    const int32_t li = lens[tid];
     int64_t rk = 0;
     for (int j = 0; j < a.nseq; ++j) {
-      const int32_t lj = sm.u.lens[j];
+      const int32_t lj = lens[j];
       rk += (lj > li) || (lj == li && j < tid);
     }
     if (rk == rank) sm.seq = tid;
@@ -305,21 +321,326 @@ GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int
   return sm.seq;
 }
 
-__global__ __launch_bounds__(kThreads)
-void gdn_chunk_prefill_kernel(PrefillArgs a) {
+// ---- producer role (waves 4..7) --------------------------------------------------
+
+// Barrier over the four producer waves: an LDS arrival counter that grows by
+// 4 per round.  The wait is bounded so a logic error cannot hang the GPU.
+GDN_DEVICE void producer_sync(int32_t* count, int32_t& target, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  target += 4;
+  if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int spin = 0; spin < kSpinLimit; ++spin) {
+    if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// A chunk's inputs in flight in registers.
+struct ChunkLoad {
+  bf16x8 k[4], q[4], v[4];
+  float g, b;  // wave 4 only: token `lane`
+};
+
+GDN_DEVICE void load_chunk(ChunkLoad& cl, const PrefillArgs& a, const bf16_t* kg, const bf16_t* qg,
+                           const bf16_t* vg, int h, int64_t c0, int64_t e, int ptid, int pw, int lane) {
+  const int64_t rem = e - c0;
+  const int Lc = (int)(rem < C ? rem : C);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int vec = ptid + u * kRoleThreads;
+    const int row = vec >> 4, cg = vec & 15;
+    if (row < Lc) {
+      const int64_t t = c0 + row;
+      cl.k[u] = *reinterpret_cast<const bf16x8*>(kg + t * a.k_s0 + 8 * cg);
+      cl.q[u] = *reinterpret_cast<const bf16x8*>(qg + t * a.q_s0 + 8 * cg);
+      cl.v[u] = *reinterpret_cast<const bf16x8*>(vg + t * a.v_s0 + 8 * cg);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) { cl.k[u][m] = (bf16_t)0.f; cl.q[u][m] = (bf16_t)0.f; cl.v[u][m] = (bf16_t)0.f; }
+    }
+  }
+  cl.g = 0.f;
+  cl.b = 0.f;
+  if (pw == 0 && lane < Lc) {
+    cl.g = a.g[(c0 + lane) * a.g_s0 + h * a.g_s1];
+    cl.b = load_scalar_f32(a.beta, (c0 + lane) * a.b_s0 + h * a.b_s1, a.b_dtype);
+  }
+}
+
+// (K K^T) tile (mt, nt) -> A = strict_lower(beta_i G_ij e^(g_i - g_j)) in fp32
+GDN_DEVICE void kk_tile(ChunkSlot& cs, int mt, int nt, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
+  f32x16 G = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KD / 16; ++ks)
+    G = mfma32(frag_rows(cs.k, LDK, 32 * mt, 16 * ks, lane), frag_rows(cs.k, LDK, 32 * nt, 16 * ks, lane), G);
+  const int j = 32 * nt + n;
+  const float gj = cs.gam[j];
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) {
+    const f32x4 gi = rows4(cs.gam, 32 * mt, i4, lane);
+    const f32x4 bi = rows4(cs.beta, 32 * mt, i4, lane);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+      cs.u.a[i * LDA + j] = i > j ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+    }
+  }
+}
+
+// (Q K^T) tile (mt, nt) -> P = lower(QK^T e^(g_i - g_j)) in fp16
+GDN_DEVICE void qk_tile(ChunkSlot& cs, int mt, int nt, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
+  f32x16 G = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KD / 16; ++ks)
+    G = mfma32(frag_rows(cs.q, LDK, 32 * mt, 16 * ks, lane), frag_rows(cs.k, LDK, 32 * nt, 16 * ks, lane), G);
+  const int j = 32 * nt + n;
+  const float gj = cs.gam[j];
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) {
+    const f32x4 gi = rows4(cs.gam, 32 * mt, i4, lane);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+      cs.p[i * LDH + j] = (f16_t)(i >= j ? G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
+    }
+  }
+}
+
+// Everything of a chunk that does not depend on the state, written to slot cs.
+GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t* count, int32_t& target,
+                              int ptid, int pw, int lane) {
+  // stage K, Q (to fp16) and V; gamma = in-chunk cumsum of g (wave 4, one token per lane)
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int vec = ptid + u * kRoleThreads;
+    const int row = vec >> 4, cg = vec & 15;
+    f16x8 k16, q16;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) { k16[m] = (f16_t)(float)cl.k[u][m]; q16[m] = (f16_t)(float)cl.q[u][m]; }
+    *reinterpret_cast<f16x8*>(cs.k + row * LDK + 8 * cg) = k16;
+    *reinterpret_cast<f16x8*>(cs.q + row * LDK + 8 * cg) = q16;
+    *reinterpret_cast<bf16x8*>(cs.v + row * LDV + 8 * cg) = cl.v[u];
+  }
+  if (pw == 0) {
+    float gm = cl.g;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(gm, off, 64);
+      if (lane >= off) gm += y;
+    }
+    const float gl = __shfl(gm, 63, 64);  // padded g is 0, so this is gamma at token L-1
+    cs.gam[lane] = gm;
+    cs.eg[lane] = __expf(gm);
+    cs.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
+    cs.beta[lane] = cl.b;
+    if (lane == 0) cs.gam_last = gl;
+  }
+  producer_sync(count, target, lane);
+
+  // A tiles (0,0), (1,0), (1,1); wave 7: zero upper tiles of A and P, P tile (0,0)
+  if (pw < 3) {
+    kk_tile(cs, pw == 0 ? 0 : 1, pw == 2 ? 1 : 0, lane);
+  } else {
+    for (int x = lane; x < 32 * 32; x += 64) {
+      const int i = x >> 5, j = 32 + (x & 31);
+      cs.u.a[i * LDA + j] = 0.f;
+      cs.p[i * LDH + j] = (f16_t)0.f;
+    }
+    qk_tile(cs, 0, 0, lane);
+  }
+  producer_sync(count, target, lane);
+
+  // diagonal blocks of T (wave 4); P tiles (1,0), (1,1) (waves 5, 6)
+  if (pw == 0) {
+    invert_diag_blocks(cs.u.a, lane);
+  } else if (pw < 3) {
+    qk_tile(cs, 1, pw == 2 ? 1 : 0, lane);
+  }
+  producer_sync(count, target, lane);
+  if (pw < 2) merge16(cs.u.a, 32 * pw, lane);
+  producer_sync(count, target, lane);
+  if (pw == 0) merge32(cs.u.a, lane);
+  producer_sync(count, target, lane);
+
+  // T' = T diag(beta) as fp16 hi/lo, in place over the fp32 T
+  float tv[16];
+  const int i = ptid >> 2, j0 = 16 * (ptid & 3);
+#pragma unroll
+  for (int m = 0; m < 16; m += 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(cs.u.a + i * LDA + j0 + m);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(cs.beta + j0 + m);
+#pragma unroll
+    for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
+  }
+  f16_t th[16], tl[16];
+  split_vec<16>(tv, th, tl);
+  producer_sync(count, target, lane);
+#pragma unroll
+  for (int m = 0; m < 16; m += 4) {
+    *reinterpret_cast<f16x4*>(cs.u.t.hi + i * LDH + j0 + m) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
+    *reinterpret_cast<f16x4*>(cs.u.t.lo + i * LDH + j0 + m) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
+  }
+}
+
+// ---- state role (waves 0..3) -----------------------------------------------------
+
+// The state products of one chunk on this wave's 32 value columns; writes the
+// chunk's output rows for those columns.
+GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& a, int64_t c0, int L, int h,
+                              int wave, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
+  const int col = 32 * wave + n;
+  const int es = wave_scale_exp(S, 4);
+  const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
+  f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    f16x8 shi, slo;
+    split8(S[ks >> 1], ks & 1, ss, shi, slo);
+    const f16x8 ak0 = frag_rows(cs.k, LDK, 0, 16 * ks, lane);
+    const f16x8 ak1 = frag_rows(cs.k, LDK, 32, 16 * ks, lane);
+    const f16x8 aq0 = frag_rows(cs.q, LDK, 0, 16 * ks, lane);
+    const f16x8 aq1 = frag_rows(cs.q, LDK, 32, 16 * ks, lane);
+    X[0] = mfma32(ak0, shi, X[0]);
+    X[1] = mfma32(ak1, shi, X[1]);
+    QS[0] = mfma32(aq0, shi, QS[0]);
+    QS[1] = mfma32(aq1, shi, QS[1]);
+    X[0] = mfma32(ak0, slo, X[0]);
+    X[1] = mfma32(ak1, slo, X[1]);
+  }
+  // R = V - diag(e^gamma) X (X, QS in units of 2^-es; V read transposed: rows are tokens)
+  const float us = __builtin_amdgcn_ldexpf(1.f, es);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 egv = rows4(cs.eg, 32 * mt, i, lane);
+      const int j = lane & 15, qd = lane >> 4;
+      const bf16_t* p = cs.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
+      const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = (float)vv[rr] - egv[rr] * (X[mt][4 * i + rr] * us);
+    }
+  }
+  f32x16* R = X;  // X now holds R
+  const int er = wave_scale_exp(R, 2);
+  const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
+  // V' = T' R, in units of 2^-er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
+  f32x16 VN[2] = {zero16(), zero16()};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    f16x8 rhi, rlo;
+    split8(R[ks >> 1], ks & 1, rs, rhi, rlo);
+    if (ks < 2) {
+      const f16x8 ah0 = frag_rows(cs.u.t.hi, LDH, 0, 16 * ks, lane);
+      const f16x8 al0 = frag_rows(cs.u.t.lo, LDH, 0, 16 * ks, lane);
+      const f16x8 ah1 = frag_rows(cs.u.t.hi, LDH, 32, 16 * ks, lane);
+      const f16x8 al1 = frag_rows(cs.u.t.lo, LDH, 32, 16 * ks, lane);
+      VN[0] = mfma32(ah0, rhi, VN[0]);
+      VN[1] = mfma32(ah1, rhi, VN[1]);
+      VN[0] = mfma32(ah0, rlo, VN[0]);
+      VN[1] = mfma32(ah1, rlo, VN[1]);
+      VN[0] = mfma32(al0, rhi, VN[0]);
+      VN[1] = mfma32(al1, rhi, VN[1]);
+    } else {
+      const f16x8 ah1 = frag_rows(cs.u.t.hi, LDH, 32, 16 * ks, lane);
+      const f16x8 al1 = frag_rows(cs.u.t.lo, LDH, 32, 16 * ks, lane);
+      VN[1] = mfma32(ah1, rhi, VN[1]);
+      VN[1] = mfma32(ah1, rlo, VN[1]);
+      VN[1] = mfma32(al1, rhi, VN[1]);
+    }
+  }
+  // O = scale (diag(e^gamma) Q S + P V')
+  const float ru = __builtin_amdgcn_ldexpf(1.f, er);
+  const float qsu = __builtin_amdgcn_ldexpf(1.f, es - er);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 egv = rows4(cs.eg, 32 * mt, i, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) QS[mt][4 * i + rr] *= egv[rr] * qsu;
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    f16x8 vb;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) vb[m] = (f16_t)VN[ks >> 1][8 * (ks & 1) + m];
+#pragma unroll
+    for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(cs.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
+  }
+  // stage this wave's output columns (bf16) in the V tile, then store 16-byte row pieces
+  {
+    const float osc = ru * a.scale;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
+        cs.v[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 16 * u + (lane >> 2), cgp = lane & 3;
+      if (row < L)
+        *reinterpret_cast<bf16x8*>(a.out + (c0 + row) * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * cgp) =
+            *reinterpret_cast<const bf16x8*>(cs.v + row * LDV + 32 * wave + 8 * cgp);
+    }
+  }
+  // S = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 dv = rows4(cs.edec, 32 * mt, i, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) VN[mt][4 * i + rr] *= dv[rr];
+    }
+  }
+  const int ed = wave_scale_exp(VN, 2);
+  const float ds = __builtin_amdgcn_ldexpf(1.f, -ed);
+  // accumulate in units of 2^-(er + ed): S_acc = e^gamma_L S 2^-(er+ed) + K^T Vd_scaled
+  const float sin_ = __expf(cs.gam_last) * __builtin_amdgcn_ldexpf(1.f, -(er + ed));
+  const float sout = __builtin_amdgcn_ldexpf(1.f, er + ed);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S[mt][j] *= sin_;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    f16x8 dhi, dlo;
+    split8(VN[ks >> 1], ks & 1, ds, dhi, dlo);
+    f16x8 akt[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(cs.k, LDK, 32 * mt, 16 * ks, lane);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dhi, S[mt]);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dlo, S[mt]);
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S[mt][j] *= sout;
+}
+
+__global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
   __shared__ Smem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int n = lane & 31;
-  const int gq = lane >> 5;
 
   // Work id: consecutive v-heads (sharing a k-head) go to one XCD (workgroups
   // are dealt round-robin over the 8 XCDs), sequences longest first.
   const int64_t bid = blockIdx.x;
   const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
   if (work >= a.nseq * a.Hv) return;
+  if (tid == 0) sm.producer_count = 0;
   const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
   const int h = (int)(work % a.Hv);
   const int kh = h / a.r;
@@ -336,292 +657,49 @@ void gdn_chunk_prefill_kernel(PrefillArgs a) {
     }
     return;
   }
+  const int nc = (int)((e - s + C - 1) / C);
+  auto chunk_len = [&](int c) { const int64_t r = e - (s + (int64_t)c * C); return (int)(r < C ? r : C); };
 
-  // ---- state S (K x V fp32) in C layout: m-tile mt holds keys 32mt.., this wave's 32 columns
-  float* Sg = a.state + slot * a.st_slot + h * a.st_head;
-  const int col = 32 * wave + n;
-  f32x16 S[4];
+  // Both roles execute exactly 1 + nc workgroup barriers.
+  if (wave < 4) {
+    // ---- state waves: S (K x V fp32) in C layout, m-tile mt = keys 32mt.., this wave's 32 columns
+    const int n = lane & 31, gq = lane >> 5;
+    const int col = 32 * wave + n;
+    float* Sg = a.state + slot * a.st_slot + h * a.st_head;
+    f32x16 S[4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
-
-  const bf16_t* qg = a.q + kh * a.q_s1;
-  const bf16_t* kg = a.k + kh * a.k_s1;
-  const bf16_t* vg = a.v + h * a.v_s1;
-
-  // the next chunk's inputs, prefetched into registers
-  bf16x8 pk[4], pq[4], pv[4];
-  float pgv = 0.f, pbv = 0.f;
-  auto prefetch = [&](int64_t c0) {
-    const int64_t rem = e - c0;
-    const int Lc = (int)(rem < C ? rem : C);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vec = tid + u * kThreads;
-      const int row = vec >> 4, cg = vec & 15;
-      if (row < Lc) {
-        const int64_t t = c0 + row;
-        pk[u] = *reinterpret_cast<const bf16x8*>(kg + t * a.k_s0 + 8 * cg);
-        pq[u] = *reinterpret_cast<const bf16x8*>(qg + t * a.q_s0 + 8 * cg);
-        pv[u] = *reinterpret_cast<const bf16x8*>(vg + t * a.v_s0 + 8 * cg);
-      } else {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) { pk[u][m] = (bf16_t)0.f; pq[u][m] = (bf16_t)0.f; pv[u][m] = (bf16_t)0.f; }
-      }
+      for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
+    __syncthreads();  // chunk 0 is prepared
+    for (int c = 0; c < nc; ++c) {
+      consume_chunk(sm.slot[c & 1], S, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
+      __syncthreads();  // slot (c & 1) is free again, slot ((c + 1) & 1) is prepared
     }
-    if (wave == 0) {
-      pgv = 0.f;
-      pbv = 0.f;
-      if (lane < Lc) {
-        pgv = a.g[(c0 + lane) * a.g_s0 + h * a.g_s1];
-        pbv = load_scalar_f32(a.beta, (c0 + lane) * a.b_s0 + h * a.b_s1, a.b_dtype);
-      }
-    }
-  };
-  prefetch(s);
-
-  for (int64_t c0 = s; c0 < e; c0 += C) {
-    const int L = (int)((e - c0) < C ? (e - c0) : C);
-    __syncthreads();  // every LDS buffer of the previous chunk is free
-
-    // ---- stage the chunk: K, Q to fp16, V as is; gamma = in-chunk cumsum of g (wave 0)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vec = tid + u * kThreads;
-      const int row = vec >> 4, cg = vec & 15;
-      f16x8 k16, q16;
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int m = 0; m < 8; ++m) { k16[m] = (f16_t)(float)pk[u][m]; q16[m] = (f16_t)(float)pq[u][m]; }
-      *reinterpret_cast<f16x8*>(sm.k + row * LDK + 8 * cg) = k16;
-      *reinterpret_cast<f16x8*>(sm.q + row * LDK + 8 * cg) = q16;
-      *reinterpret_cast<bf16x8*>(sm.v + row * LDV + 8 * cg) = pv[u];
-    }
-    if (wave == 0) {
-      float gm = pgv;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(gm, off, 64);
-        if (lane >= off) gm += y;
-      }
-      const float gl = __shfl(gm, 63, 64);  // padded g is 0, so this is gamma at token L-1
-      sm.gam[lane] = gm;
-      sm.eg[lane] = __expf(gm);
-      sm.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
-      sm.beta[lane] = pbv;
-      if (lane == 0) sm.gam_last = gl;
-    }
+      for (int j = 0; j < 16; ++j) Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = S[mt][j];
+  } else {
+    // ---- producer waves: chunk c + 1 while the state waves work on chunk c
+    const int ptid = tid - kRoleThreads, pw = wave - 4;
+    const bf16_t* qg = a.q + kh * a.q_s1;
+    const bf16_t* kg = a.k + kh * a.k_s1;
+    const bf16_t* vg = a.v + h * a.v_s1;
+    int32_t target = 0;
+    ChunkLoad cl;
+    load_chunk(cl, a, kg, qg, vg, h, s, e, ptid, pw, lane);
+    prepare_chunk(sm.slot[0], cl, chunk_len(0), &sm.producer_count, target, ptid, pw, lane);
+    if (nc > 1) load_chunk(cl, a, kg, qg, vg, h, s + C, e, ptid, pw, lane);
     __syncthreads();
-
-    // ---- A = strict_lower(beta_i (K K^T)_ij e^(g_i - g_j)): 32x32 tiles (0,0), (1,0), (1,1)
-    if (wave < 3) {
-      const int mt = wave == 0 ? 0 : 1;
-      const int nt = wave == 2 ? 1 : 0;
-      f32x16 G = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KD / 16; ++ks)
-        G = mfma32(frag_rows(sm.k, LDK, 32 * mt, 16 * ks, lane), frag_rows(sm.k, LDK, 32 * nt, 16 * ks, lane), G);
-      const int j = 32 * nt + n;
-      const float gj = sm.gam[j];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4 gi = rows4(sm.gam, 32 * mt, i4, lane);
-        const f32x4 bi = rows4(sm.beta, 32 * mt, i4, lane);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
-          sm.u.a[i * LDA + j] = i > j ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
-        }
+    for (int c = 0; c < nc; ++c) {
+      if (c + 1 < nc) {
+        prepare_chunk(sm.slot[(c + 1) & 1], cl, chunk_len(c + 1), &sm.producer_count, target, ptid, pw, lane);
+        if (c + 2 < nc) load_chunk(cl, a, kg, qg, vg, h, s + (int64_t)(c + 2) * C, e, ptid, pw, lane);
       }
-    } else {  // upper 32x32 tile of A and P are zero
-      for (int x = lane; x < 32 * 32; x += 64) {
-        const int i = x >> 5, j = 32 + (x & 31);
-        sm.u.a[i * LDA + j] = 0.f;
-        sm.p[i * LDH + j] = (f16_t)0.f;
-      }
-    }
-    __syncthreads();
-
-    // ---- wave 0: diagonal blocks of T; waves 1-3: P = lower(Q K^T e^(g_i - g_j))
-    if (wave == 0) {
-      invert_diag_blocks(sm.u.a, lane);
-    } else {
-      const int mt = wave == 1 ? 0 : 1;
-      const int nt = wave == 3 ? 1 : 0;
-      f32x16 Pq = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KD / 16; ++ks)
-        Pq = mfma32(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), frag_rows(sm.k, LDK, 32 * nt, 16 * ks, lane), Pq);
-      const int j = 32 * nt + n;
-      const float gj = sm.gam[j];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4 gi = rows4(sm.gam, 32 * mt, i4, lane);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
-          sm.p[i * LDH + j] = (f16_t)(i >= j ? Pq[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
-        }
-      }
-    }
-    __syncthreads();
-    if (wave < 2) merge16(sm.u.a, 32 * wave, lane);
-    __syncthreads();
-    if (wave == 0) merge32(sm.u.a, lane);
-    __syncthreads();
-    // ---- T' = T diag(beta) as fp16 hi/lo, in place over the fp32 T
-    {
-      float tv[16];
-      const int i = tid >> 2, j0 = 16 * (tid & 3);
-#pragma unroll
-      for (int m = 0; m < 16; m += 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(sm.u.a + i * LDA + j0 + m);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(sm.beta + j0 + m);
-#pragma unroll
-        for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
-      }
-      f16_t th[16], tl[16];
-      split_vec<16>(tv, th, tl);
       __syncthreads();
-#pragma unroll
-      for (int m = 0; m < 16; m += 4) {
-        *reinterpret_cast<f16x4*>(sm.u.t.hi + i * LDH + j0 + m) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
-        *reinterpret_cast<f16x4*>(sm.u.t.lo + i * LDH + j0 + m) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
-      }
-    }
-    __syncthreads();
-
-    if (c0 + C < e) prefetch(c0 + C);
-
-    // ---- per-wave state products on this wave's 32 value columns
-    const int es = wave_scale_exp(S, 4);
-    const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
-    f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      f16x8 shi, slo;
-      split8(S[ks >> 1], ks & 1, ss, shi, slo);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const f16x8 ak = frag_rows(sm.k, LDK, 32 * mt, 16 * ks, lane);
-        X[mt] = mfma32(ak, shi, X[mt]);
-        X[mt] = mfma32(ak, slo, X[mt]);
-        QS[mt] = mfma32(frag_rows(sm.q, LDK, 32 * mt, 16 * ks, lane), shi, QS[mt]);
-      }
-    }
-    // R = V - diag(e^gamma) X (X, QS in units of 2^-es; V read transposed: rows are tokens)
-    const float us = __builtin_amdgcn_ldexpf(1.f, es);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 egv = rows4(sm.eg, 32 * mt, i, lane);
-        const int j = lane & 15, qd = lane >> 4;
-        const bf16_t* p = sm.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
-        const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = (float)vv[rr] - egv[rr] * (X[mt][4 * i + rr] * us);
-      }
-    }
-    f32x16* R = X;  // X now holds R
-    const int er = wave_scale_exp(R, 2);
-    const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
-    // V' = T' R, in units of 2^-er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
-    f32x16 VN[2] = {zero16(), zero16()};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      f16x8 rhi, rlo;
-      split8(R[ks >> 1], ks & 1, rs, rhi, rlo);
-#pragma unroll
-      for (int mt = (ks >> 1); mt < 2; ++mt) {
-        const f16x8 ah = frag_rows(sm.u.t.hi, LDH, 32 * mt, 16 * ks, lane);
-        const f16x8 al = frag_rows(sm.u.t.lo, LDH, 32 * mt, 16 * ks, lane);
-        VN[mt] = mfma32(ah, rhi, VN[mt]);
-        VN[mt] = mfma32(ah, rlo, VN[mt]);
-        VN[mt] = mfma32(al, rhi, VN[mt]);
-      }
-    }
-    // O = scale (diag(e^gamma) Q S + P V'), staged as bf16 in this wave's columns of sm.v
-    const float ru = __builtin_amdgcn_ldexpf(1.f, er);
-    const float qsu = __builtin_amdgcn_ldexpf(1.f, es - er);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 egv = rows4(sm.eg, 32 * mt, i, lane);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) QS[mt][4 * i + rr] *= egv[rr] * qsu;
-      }
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      f16x8 vb;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) vb[m] = (f16_t)VN[ks >> 1][8 * (ks & 1) + m];
-#pragma unroll
-      for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(sm.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
-    }
-    {
-      const float osc = ru * a.scale;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-          const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
-          sm.v[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
-        }
-    }
-    // S = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 dv = rows4(sm.edec, 32 * mt, i, lane);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) VN[mt][4 * i + rr] *= dv[rr];
-      }
-    }
-    const int ed = wave_scale_exp(VN, 2);
-    const float ds = __builtin_amdgcn_ldexpf(1.f, -ed);
-    // accumulate in units of 2^-(er + ed): S_acc = e^gamma_L S 2^-(er+ed) + K^T Vd_scaled
-    const float sin_ = __expf(sm.gam_last) * __builtin_amdgcn_ldexpf(1.f, -(er + ed));
-    const float sout = __builtin_amdgcn_ldexpf(1.f, er + ed);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) S[mt][j] *= sin_;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      f16x8 dhi, dlo;
-      split8(VN[ks >> 1], ks & 1, ds, dhi, dlo);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const f16x8 akt = frag_cols(sm.k, LDK, 32 * mt, 16 * ks, lane);
-        S[mt] = mfma32(akt, dhi, S[mt]);
-        S[mt] = mfma32(akt, dlo, S[mt]);
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) S[mt][j] *= sout;
-    __syncthreads();
-    // ---- store the chunk's output rows
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vec = tid + u * kThreads;
-      const int row = vec >> 4, cg = vec & 15;
-      if (row < L)
-        *reinterpret_cast<bf16x8*>(a.out + (c0 + row) * a.o_s0 + h * a.o_s1 + 8 * cg) =
-            *reinterpret_cast<const bf16x8*>(sm.v + row * LDV + 8 * cg);
     }
   }
-
-  // ---- final state back to the slot
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = S[mt][j];
 }
 
 }  // namespace
