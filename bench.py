@@ -35,6 +35,22 @@ HK, HV, DK, DV, CHUNK = 16, 32, 128, 128, 64
 # algorithmic FLOPs per prefill token: KK^T and QK^T once per k-head (C x C x K),
 # per v-head w, u, A_qk v', w S, k^T v', q S (2 C V + C K + 3 K V), x2 for FMA
 PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK + 3 * DK * DV) * HV)
+# HBM bytes per launch of each kernel on this benchmark's workloads, from
+# rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch), each
+# scaled by what the same counter reads on a plain 1 GiB device copy
+# (--workload hbm_copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0 on MI355X).  Values
+# from the committed profiles of the current kernels; a kernel without an
+# entry reports None.
+HBM_TRAFFIC_PER_LAUNCH = {
+    "gdn_chunk_prefill_kernel": 1_052_598_584,
+    "gdn_recurrent_step_kernel": 1_083_318_318,
+    "causal_conv1d_varlen_kernel": 680_914_206,
+    "causal_conv1d_step_kernel": 59_431_379,
+}
+
+
+def _traffic(kernel: str):
+    return HBM_TRAFFIC_PER_LAUNCH.get(kernel)
 
 
 def _cpu_threads() -> int:
@@ -108,7 +124,7 @@ def bench_prefill(dev, steps, warmup, cpu_budget):
         "kernel_ms": kern_ms,
         "tokens_per_s": T / (ms * 1e-3),
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": _traffic("gdn_chunk_prefill_kernel"),
                      "flop_per_launch": flop, "kernel": "gdn_chunk_prefill_kernel"},
     }
     if cpu_budget > 0:
@@ -150,7 +166,8 @@ def bench_decode(dev, steps, warmup, cpu_budget):
         "kernel_ms": kern_ms,
         "GB_per_s": gbs,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                     "traffic": None, "bytes_per_launch": nbytes, "kernel": "gdn_recurrent_step_kernel"},
+                     "traffic": _traffic("gdn_recurrent_step_kernel"), "bytes_per_launch": nbytes,
+                     "kernel": "gdn_recurrent_step_kernel"},
     }
     if cpu_budget > 0:
         from oracle.gdn import recurrent_gated_delta_rule_ref
@@ -183,8 +200,8 @@ def bench_conv(dev, steps, warmup, cpu_budget):
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     res = {"tokens": T, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
-                        "kernel": "causal_conv1d_varlen_kernel"}}
+                        "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("causal_conv1d_varlen_kernel"),
+                        "bytes_per_launch": nbytes, "kernel": "causal_conv1d_varlen_kernel"}}
     if cpu_budget > 0:
         from oracle.conv import causal_conv1d_fn_ref
 
@@ -215,8 +232,27 @@ def bench_conv_update(dev, steps, warmup, cpu_budget):
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("causal_conv1d_step_kernel"),
+                         "bytes_per_launch": nbytes, "kernel": "causal_conv1d_step_kernel"}}
+
+
+def bench_hbm_copy(dev, steps, warmup, cpu_budget):
+    """Plain 1 GiB device-to-device copy: the calibration point of the HBM
+    byte counters and the copy bandwidth this device reaches."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_()
+    dst = torch.empty_like(src)
+
+    def step(_):
+        dst.copy_(src)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    nbytes = 2 * n
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    return {"bytes": nbytes, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
-                         "kernel": "causal_conv1d_step_kernel"}}
+                         "kernel": "torch elementwise copy"}}
 
 
 def main():
@@ -224,7 +260,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update"], default="all")
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update", "hbm_copy"], default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     args = ap.parse_args()
@@ -253,6 +289,8 @@ def main():
     if want("conv_update"):
         parts["conv_update"] = bench_conv_update(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# conv_update: {parts['conv_update']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if args.workload == "hbm_copy":
+        parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
 
     head_name = "prefill" if "prefill" in parts else next(iter(parts))
     head = parts.pop(head_name)
@@ -263,6 +301,9 @@ def main():
     elif head_name == "decode":
         metric, value, unit = "GDN decode state-update HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "gdn_recurrent_step: batch 256 from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128"
+    elif head_name == "hbm_copy":
+        metric, value, unit = "device copy HBM GB/s", head["GB_per_s"], "GB/s"
+        workload = "hbm_copy: 1 GiB device-to-device copy (read + write counted)"
     else:
         metric, value, unit = f"causal_conv1d {head_name} HBM GB/s", head["GB_per_s"], "GB/s"
         workload = f"causal_conv1d {head_name}: 8192 channels, width 4, bf16 x/w, fp32 conv state"

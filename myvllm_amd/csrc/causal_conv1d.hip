@@ -6,7 +6,7 @@
 // yuyifanbupt/myvllm).  Both are HBM-streaming kernels: each thread owns 8
 // consecutive channels (one 16-byte bf16 vector) and walks tokens, keeping
 // the W-1 previous inputs in registers, so x is read once (plus a W-1 row
-// halo per 64-token tile) and y written once, fully coalesced.
+// halo per 32-token tile) and y written once, fully coalesced.
 //
 // Prefill tiling: each sequence is cut into 32-token tiles; blockIdx.x is a
 // linear tile id resolved to (sequence, tile) on the device, so no host sync
