@@ -13,27 +13,31 @@
 //    value columns [32w, 32w+32)) and run the state products of chunk c;
 //  * producer waves 4..7 stage chunk c+1 (K, Q, V, decays) into the other
 //    slot and compute everything that does not depend on the state: the
-//    kk^T and qk^T tiles, A, T = (I + A)^-1 diag(beta) and P.
+//    kk^T and qk^T tiles, T' = (I + A)^-1 diag(beta) and P.  Waves 4 and 5
+//    each solve one 32x32 diagonal block of T' on their own, wave 6 forms
+//    B_10 and a P tile, wave 7 the other P tiles; after one producer barrier
+//    wave 4 forms the off-diagonal block T'_10 = -T'_11 B_10 T'_00.
 // Both roles execute one workgroup barrier per chunk; producers synchronise
-// among themselves through an LDS counter.
+// among themselves through an LDS counter (two rounds per chunk).
 //
 // Per chunk of L <= 64 tokens (gamma = in-chunk cumsum of g):
 //   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kk^T, MFMA)
 //   P  = lower(q_i.k_j e^(gamma_i - gamma_j))                  (qk^T, MFMA)
-//   T  = (I + A)^-1 diag(beta)     (16x16 diagonal blocks by substitution,
+//   T' = (I + A)^-1 diag(beta)    (16x16 diagonal blocks by substitution,
 //                                   off-diagonal blocks by MFMA block merges)
 //   R  = V - diag(e^gamma) K S
-//   V' = T R                       (= u - w S of the reference)
+//   V' = T' R                      (= u - w S of the reference)
 //   O  = scale [diag(e^gamma) Q S + P V']
 //   S  = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
 //
 // The MFMAs run in fp16 (same rate as bf16): q and k are L2-normalised bf16
 // values, which fp16 holds exactly, and every fp32 operand that feeds the
-// carried state (S, R, the decayed V', T and the merge operands) is split
-// into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  Split
-// operands are first scaled by a per-wave power of two (max |x| in
+// carried state (S, R, the decayed V', T', B_10 and the merge product) is
+// split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  S, R
+// and V' are first scaled by a per-wave power of two (max |x| in
 // [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
-// undone on the fp32 accumulator.  Products that only feed o use the hi part.
+// undone on the fp32 accumulator.  The T' blocks and B_10 (|B_10| <= 1) are
+// split unscaled.  Products that only feed o use the hi part.
 //
 // MFMA operand layouts (lane l, n = l % 32, g = l / 32), 32x32x16:
 // A[m][k] lane holds row n, 8 k; B[k][n] lane holds column n, 8 k; C lane
@@ -54,7 +58,7 @@ constexpr int KD = 128;    // key head dim
 constexpr int VD = 128;    // value head dim
 constexpr int LDK = 136;   // fp16 row stride of the K/Q tiles
 constexpr int LDV = 144;   // bf16 row stride of the V tile (conflict-free transposed reads)
-constexpr int LDA = 68;    // fp32 row stride of A/T
+constexpr int LDS32 = 32;  // fp32 row stride of a 32x32 diagonal block being solved (rows 16-byte aligned)
 constexpr int LDH = 68;    // fp16 row stride of T_hi/T_lo/P
 constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this many sequences
 constexpr int kSpinLimit = 1 << 22;  // bound on a producer barrier wait (never reached when correct)
@@ -82,13 +86,17 @@ struct ChunkSlot {
   f16_t q[C * LDK];
   bf16_t v[C * LDV];  // chunk values, then the staging buffer of the chunk's output
   union {
-    float a[C * LDA];  // A, then T = (I + A)^-1 in place
     struct {
-      f16_t hi[C * LDH];  // T' = T diag(beta), hi part
-      f16_t lo[C * LDH];  // lo part
+      // T' = (I + A)^-1 diag(beta) as fp16 hi + lo.  Block (0,1) (rows 0..31,
+      // columns 32..63) of T' is zero and never read by the state waves; the
+      // producers keep B_10 there (see prepare_chunk).
+      f16_t hi[C * LDH];
+      f16_t lo[C * LDH];
     } t;
     int32_t lens[kMaxRankedSeqs];  // sequence lengths, before the first chunk
   } u;
+  // P (fp16).  Before P is written, the two 32x32 diagonal blocks of A are
+  // solved here in fp32 (2 x 32 rows of LDS32 floats).
   f16_t p[C * LDH];
   alignas(16) float gam[C];
   alignas(16) float eg[C];    // e^gamma
@@ -96,6 +104,7 @@ struct ChunkSlot {
   alignas(16) float beta[C];
   float gam_last;
 };
+static_assert(2 * 32 * LDS32 * sizeof(float) <= sizeof(f16_t) * C * LDH, "solve scratch must fit the P region");
 
 struct Smem {
   ChunkSlot slot[2];
@@ -197,13 +206,22 @@ GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
   for (int m = 0; m < N; m += 2) split_pair(x[m], x[m + 1], hi[m], hi[m + 1], lo[m], lo[m + 1]);
 }
 
-// ---- T = (I + A)^-1 pieces (A strictly lower, fp32 in LDS) --------------------
+// ---- T' = (I + A)^-1 diag(beta) pieces -------------------------------------------
+//
+// With B = strict_lower(k_i.k_j e^(gamma_i - gamma_j)) and A = diag(beta) B,
+// T' = (I + diag(beta) B)^-1 diag(beta) is block lower triangular over the two
+// 32-token halves, and its off-diagonal block satisfies
+//   T'_10 = -T'_11 B_10 T'_00,
+// so each diagonal block is solved on its own (one wave each) and the
+// off-diagonal block needs only the fp16 hi/lo of T'_00, T'_11 and B_10.
 
-// Diagonal 16x16 blocks by right-looking forward substitution; lane (b, c)
-// = (lane / 16, lane % 16) computes column c of block b.  One wave.
-GDN_DEVICE void invert_diag_blocks(float* A, int lane) {
-  const int b = lane >> 4, c = lane & 15;
-  float* Ab = A + 16 * b * LDA + 16 * b;
+// 16x16 diagonal blocks of a 32x32 strictly lower block A (fp32, stride
+// LDS32) by right-looking forward substitution, in place: lane (b, c) =
+// ((lane / 16) % 2, lane % 16) computes column c of block b; lanes 32..63
+// repeat lanes 0..31 and do not store.
+GDN_DEVICE void invert_diag16(float* A, int lane) {
+  const int b = (lane >> 4) & 1, c = lane & 15;
+  float* Ab = A + 16 * b * LDS32 + 16 * b;
   float y[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) y[i] = i == c ? 1.f : 0.f;
@@ -211,10 +229,12 @@ GDN_DEVICE void invert_diag_blocks(float* A, int lane) {
   for (int kk = 0; kk < 15; ++kk) {
     const float xk = y[kk];
 #pragma unroll
-    for (int i = kk + 1; i < 16; ++i) y[i] = fmaf(-Ab[i * LDA + kk], xk, y[i]);
+    for (int i = kk + 1; i < 16; ++i) y[i] = fmaf(-Ab[i * LDS32 + kk], xk, y[i]);
   }
+  if (lane < 32) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) Ab[i * LDA + c] = y[i];
+    for (int i = 0; i < 16; ++i) Ab[i * LDS32 + c] = y[i];
+  }
 }
 
 GDN_DEVICE void split4(f32x4 x, f16x4& hi, f16x4& lo) {
@@ -225,17 +245,17 @@ GDN_DEVICE void split4(f32x4 x, f16x4& hi, f16x4& lo) {
   lo = (f16x4){l[0], l[1], l[2], l[3]};
 }
 
-// 16 -> 32 merge: T_10 = -T_11 A_10 T_00 for the 32-block starting at row and
-// column o (0 or 32), with 16x16x16 MFMAs on hi/lo splits.  One wave.
-GDN_DEVICE void merge16(float* A, int o, int lane) {
+// 16 -> 32 merge inside a 32x32 block whose diagonal 16-blocks hold their
+// inverses: T_10 = -T_11 A_10 T_00, with 16x16x16 MFMAs on hi/lo splits.
+GDN_DEVICE void merge16(float* A, int lane) {
   const int n = lane & 15, g4 = 4 * (lane >> 4);
   f16x4 ah, al, bh, bl;
   // M = A_10 T_00: A operand = rows of A_10, B operand = columns of T_00
-  split4(*reinterpret_cast<const f32x4*>(A + (o + 16 + n) * LDA + o + g4), ah, al);
+  split4(*reinterpret_cast<const f32x4*>(A + (16 + n) * LDS32 + g4), ah, al);
   {
     f32x4 y;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) y[m] = A[(o + g4 + m) * LDA + o + n];
+    for (int m = 0; m < 4; ++m) y[m] = A[(g4 + m) * LDS32 + n];
     split4(y, bh, bl);
   }
   f32x4 M = {0.f, 0.f, 0.f, 0.f};
@@ -243,57 +263,14 @@ GDN_DEVICE void merge16(float* A, int o, int lane) {
   M = mfma16(ah, bl, M);
   M = mfma16(al, bh, M);
   // T_10 = -T_11 M: A operand = rows of T_11, B operand = M (C layout rows == k)
-  split4(*reinterpret_cast<const f32x4*>(A + (o + 16 + n) * LDA + o + 16 + g4), ah, al);
+  split4(*reinterpret_cast<const f32x4*>(A + (16 + n) * LDS32 + 16 + g4), ah, al);
   split4(M, bh, bl);
   f32x4 R = {0.f, 0.f, 0.f, 0.f};
   R = mfma16(ah, bh, R);
   R = mfma16(ah, bl, R);
   R = mfma16(al, bh, R);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) A[(o + 16 + g4 + m) * LDA + o + n] = -R[m];
-}
-
-// 32 -> 64 merge: T_10 = -T_11 A_10 T_00 with 32x32 blocks, 32x32x16 MFMAs on
-// hi/lo splits.  One wave.
-GDN_DEVICE void merge32(float* A, int lane) {
-  const int n = lane & 31, g4 = 4 * (lane >> 5);
-  f32x16 M = zero16();
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    // A operand: A_10[n][16ks + slots] = A[32 + n][...]; B operand: T_00[16ks + slots][n]
-    const float* pa = A + (32 + n) * LDA + 16 * ks + g4;
-    f16x4 ah0, al0, ah1, al1, bh0, bl0, bh1, bl1;
-    split4(*reinterpret_cast<const f32x4*>(pa), ah0, al0);
-    split4(*reinterpret_cast<const f32x4*>(pa + 8), ah1, al1);
-    f32x4 y0, y1;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      y0[m] = A[(16 * ks + g4 + m) * LDA + n];
-      y1[m] = A[(16 * ks + 8 + g4 + m) * LDA + n];
-    }
-    split4(y0, bh0, bl0);
-    split4(y1, bh1, bl1);
-    const f16x8 ah = cat4(ah0, ah1), al = cat4(al0, al1), bh = cat4(bh0, bh1), bl = cat4(bl0, bl1);
-    M = mfma32(ah, bh, M);
-    M = mfma32(ah, bl, M);
-    M = mfma32(al, bh, M);
-  }
-  f32x16 R = zero16();
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const float* pa = A + (32 + n) * LDA + 32 + 16 * ks + g4;
-    f16x4 ah0, al0, ah1, al1;
-    split4(*reinterpret_cast<const f32x4*>(pa), ah0, al0);
-    split4(*reinterpret_cast<const f32x4*>(pa + 8), ah1, al1);
-    f16x8 bh, bl;
-    split8(M, ks, 1.f, bh, bl);
-    const f16x8 ah = cat4(ah0, ah1), al = cat4(al0, al1);
-    R = mfma32(ah, bh, R);
-    R = mfma32(ah, bl, R);
-    R = mfma32(al, bh, R);
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) A[(32 + 8 * (j >> 2) + g4 + (j & 3)) * LDA + n] = -R[j];
+  for (int m = 0; m < 4; ++m) A[(16 + g4 + m) * LDS32 + n] = -R[m];
 }
 
 // Sequence of rank `rank` in longest-first order (ties by index); called by
@@ -368,48 +345,158 @@ GDN_DEVICE void load_chunk(ChunkLoad& cl, const PrefillArgs& a, const bf16_t* kg
   }
 }
 
-// (K K^T) tile (mt, nt) -> A = strict_lower(beta_i G_ij e^(g_i - g_j)) in fp32
-GDN_DEVICE void kk_tile(ChunkSlot& cs, int mt, int nt, int lane) {
-  const int n = lane & 31, gq = lane >> 5;
+// Gram tile (mt, nt) of rows of M1 against rows of M2 (K = 128): C layout,
+// lane holds column 32nt + n, rows 32mt + 8i + 4g + r.
+GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, int lane) {
   f32x16 G = zero16();
 #pragma unroll
   for (int ks = 0; ks < KD / 16; ++ks)
-    G = mfma32(frag_rows(cs.k, LDK, 32 * mt, 16 * ks, lane), frag_rows(cs.k, LDK, 32 * nt, 16 * ks, lane), G);
-  const int j = 32 * nt + n;
-  const float gj = cs.gam[j];
+    G = mfma32(frag_rows(M1, LDK, 32 * mt, 16 * ks, lane), frag_rows(M2, LDK, 32 * nt, 16 * ks, lane), G);
+  return G;
+}
+
+// Diagonal block `blk` of T': A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
+// from the kk^T tile, solved in fp32 in the wave's scratch block (16x16
+// substitution + one MFMA merge), then T'_bb = T_bb diag(beta) written as
+// fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's LDS
+// accesses complete in program order.
+GDN_DEVICE void solve_diag_block(ChunkSlot& cs, int blk, int lane) {
+  const int n = lane & 31, gq = lane >> 5, o = 32 * blk;
+  float* A = reinterpret_cast<float*>(cs.p) + blk * 32 * LDS32;
+  const f32x16 G = gram_tile(cs.k, cs.k, blk, blk, lane);
+  const float gj = cs.gam[o + n];
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
-    const f32x4 gi = rows4(cs.gam, 32 * mt, i4, lane);
-    const f32x4 bi = rows4(cs.beta, 32 * mt, i4, lane);
+    const f32x4 gi = rows4(cs.gam, o, i4, lane);
+    const f32x4 bi = rows4(cs.beta, o, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
-      cs.u.a[i * LDA + j] = i > j ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+      const int i = 8 * i4 + 4 * gq + rr;
+      A[i * LDS32 + n] = i > n ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+    }
+  }
+  invert_diag16(A, lane);
+  merge16(A, lane);
+  // T'_bb = T_bb diag(beta): lane -> row lane / 2, 16 columns
+  const int i = lane >> 1, j0 = 16 * (lane & 1);
+  float tv[16];
+#pragma unroll
+  for (int m = 0; m < 16; m += 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(A + i * LDS32 + j0 + m);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(cs.beta + o + j0 + m);
+#pragma unroll
+    for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
+  }
+  f16_t th[16], tl[16];
+  split_vec<16>(tv, th, tl);
+#pragma unroll
+  for (int m = 0; m < 16; m += 4) {
+    const int off = (o + i) * LDH + o + j0 + m;
+    *reinterpret_cast<f16x4*>(cs.u.t.hi + off) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
+    *reinterpret_cast<f16x4*>(cs.u.t.lo + off) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
+  }
+}
+
+// B_10 = k_i.k_j e^(g_i - g_j) for tokens i in 32..63, j in 0..31 (always
+// i > j), as fp16 hi/lo in block (0,1) of the T' arrays: B_10[i][j] at row i,
+// column 32 + j.  |B_10| <= 1, so the split needs no scaling.
+GDN_DEVICE void b10_block(ChunkSlot& cs, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
+  const f32x16 G = gram_tile(cs.k, cs.k, 1, 0, lane);
+  const float gj = cs.gam[n];
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) {
+    const f32x4 gi = rows4(cs.gam, 32, i4, lane);
+#pragma unroll
+    for (int rr = 0; rr < 4; rr += 2) {
+      const int i = 8 * i4 + 4 * gq + rr;
+      f16_t h0, h1, l0, l1;
+      split_pair(G[4 * i4 + rr] * __expf(gi[rr] - gj), G[4 * i4 + rr + 1] * __expf(gi[rr + 1] - gj), h0, h1, l0, l1);
+      cs.u.t.hi[i * LDH + 32 + n] = h0;
+      cs.u.t.hi[(i + 1) * LDH + 32 + n] = h1;
+      cs.u.t.lo[i * LDH + 32 + n] = l0;
+      cs.u.t.lo[(i + 1) * LDH + 32 + n] = l1;
     }
   }
 }
 
-// (Q K^T) tile (mt, nt) -> P = lower(QK^T e^(g_i - g_j)) in fp16
-GDN_DEVICE void qk_tile(ChunkSlot& cs, int mt, int nt, int lane) {
+// T'_10 = -T'_11 B_10 T'_00 from the fp16 hi/lo blocks (lo x lo dropped).  One wave.
+GDN_DEVICE void merge_offdiag(ChunkSlot& cs, int lane) {
   const int n = lane & 31, gq = lane >> 5;
-  f32x16 G = zero16();
+  const f16_t* th = cs.u.t.hi;
+  const f16_t* tl = cs.u.t.lo;
+  // M = B_10 T'_00: A operand = rows of B_10, B operand = columns of T'_00
+  f32x16 M = zero16();
 #pragma unroll
-  for (int ks = 0; ks < KD / 16; ++ks)
-    G = mfma32(frag_rows(cs.q, LDK, 32 * mt, 16 * ks, lane), frag_rows(cs.k, LDK, 32 * nt, 16 * ks, lane), G);
+  for (int ks = 0; ks < 2; ++ks) {
+    const f16x8 bh = frag_rows(th, LDH, 0, 32 + 16 * ks, lane), bl = frag_rows(tl, LDH, 0, 32 + 16 * ks, lane);
+    const f16x8 ch = frag_cols(th, LDH, 0, 16 * ks, lane), cl = frag_cols(tl, LDH, 0, 16 * ks, lane);
+    M = mfma32(bh, ch, M);
+    M = mfma32(bh, cl, M);
+    M = mfma32(bl, ch, M);
+  }
+  // -T'_11 M: A operand = rows of T'_11, B operand = M (C layout rows == k)
+  f32x16 R = zero16();
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const f16x8 ah = frag_rows(th, LDH, 32, 32 + 16 * ks, lane), al = frag_rows(tl, LDH, 32, 32 + 16 * ks, lane);
+    f16x8 mh, ml;
+    split8(M, ks, 1.f, mh, ml);
+    R = mfma32(ah, mh, R);
+    R = mfma32(ah, ml, R);
+    R = mfma32(al, mh, R);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j += 2) {
+    const int i = 32 + 8 * (j >> 2) + 4 * gq + (j & 3);
+    f16_t h0, h1, l0, l1;
+    split_pair(-R[j], -R[j + 1], h0, h1, l0, l1);
+    cs.u.t.hi[i * LDH + n] = h0;
+    cs.u.t.hi[(i + 1) * LDH + n] = h1;
+    cs.u.t.lo[i * LDH + n] = l0;
+    cs.u.t.lo[(i + 1) * LDH + n] = l1;
+  }
+}
+
+// (Q K^T) tile (mt, nt) -> P = lower(q_i.k_j e^(g_i - g_j)) as fp16, C layout
+// (element 4 i4 + rr of the tile at row 32mt + 8 i4 + 4g + rr).
+GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkSlot& cs, int mt, int nt, int h, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
   const int j = 32 * nt + n;
   const float gj = cs.gam[j];
+  f16x8 out;
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) {
+  for (int i4 = 2 * h; i4 < 2 * h + 2; ++i4) {
     const f32x4 gi = rows4(cs.gam, 32 * mt, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
-      cs.p[i * LDH + j] = (f16_t)(i >= j ? G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
+      out[4 * (i4 - 2 * h) + rr] = (f16_t)(i >= j ? G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
     }
+  }
+  return out;
+}
+struct PTile {
+  f16x8 h[2];
+};
+GDN_DEVICE PTile qk_tile(const ChunkSlot& cs, int mt, int nt, int lane) {
+  const f32x16 G = gram_tile(cs.q, cs.k, mt, nt, lane);
+  PTile t;
+  t.h[0] = qk_half(G, cs, mt, nt, 0, lane);
+  t.h[1] = qk_half(G, cs, mt, nt, 1, lane);
+  return t;
+}
+GDN_DEVICE void store_p(ChunkSlot& cs, const PTile& t, int mt, int nt, int lane) {
+  const int n = lane & 31, gq = lane >> 5;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = 32 * mt + 8 * (e >> 2) + 4 * gq + (e & 3);
+    cs.p[i * LDH + 32 * nt + n] = t.h[e >> 3][e & 7];
   }
 }
 
 // Everything of a chunk that does not depend on the state, written to slot cs.
+// Two producer barriers: after staging, and after the diagonal blocks.
 GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t* count, int32_t& target,
                               int ptid, int pw, int lane) {
   // stage K, Q (to fp16) and V; gamma = in-chunk cumsum of g (wave 4, one token per lane)
@@ -440,48 +527,28 @@ GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t
   }
   producer_sync(count, target, lane);
 
-  // A tiles (0,0), (1,0), (1,1); wave 7: zero upper tiles of A and P, P tile (0,0)
-  if (pw < 3) {
-    kk_tile(cs, pw == 0 ? 0 : 1, pw == 2 ? 1 : 0, lane);
+  // waves 4, 5: diagonal blocks of T' (scratch in the P region); wave 6: B_10
+  // and P tile (1,0); wave 7: P tiles (0,0), (1,1).  P stays in registers
+  // until the scratch is free.
+  PTile pa, pb;
+  if (pw < 2) {
+    solve_diag_block(cs, pw, lane);
+  } else if (pw == 2) {
+    b10_block(cs, lane);
+    pa = qk_tile(cs, 1, 0, lane);
   } else {
-    for (int x = lane; x < 32 * 32; x += 64) {
-      const int i = x >> 5, j = 32 + (x & 31);
-      cs.u.a[i * LDA + j] = 0.f;
-      cs.p[i * LDH + j] = (f16_t)0.f;
-    }
-    qk_tile(cs, 0, 0, lane);
+    pa = qk_tile(cs, 0, 0, lane);
+    pb = qk_tile(cs, 1, 1, lane);
   }
   producer_sync(count, target, lane);
 
-  // diagonal blocks of T (wave 4); P tiles (1,0), (1,1) (waves 5, 6)
   if (pw == 0) {
-    invert_diag_blocks(cs.u.a, lane);
-  } else if (pw < 3) {
-    qk_tile(cs, 1, pw == 2 ? 1 : 0, lane);
-  }
-  producer_sync(count, target, lane);
-  if (pw < 2) merge16(cs.u.a, 32 * pw, lane);
-  producer_sync(count, target, lane);
-  if (pw == 0) merge32(cs.u.a, lane);
-  producer_sync(count, target, lane);
-
-  // T' = T diag(beta) as fp16 hi/lo, in place over the fp32 T
-  float tv[16];
-  const int i = ptid >> 2, j0 = 16 * (ptid & 3);
-#pragma unroll
-  for (int m = 0; m < 16; m += 4) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(cs.u.a + i * LDA + j0 + m);
-    const f32x4 bb = *reinterpret_cast<const f32x4*>(cs.beta + j0 + m);
-#pragma unroll
-    for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
-  }
-  f16_t th[16], tl[16];
-  split_vec<16>(tv, th, tl);
-  producer_sync(count, target, lane);
-#pragma unroll
-  for (int m = 0; m < 16; m += 4) {
-    *reinterpret_cast<f16x4*>(cs.u.t.hi + i * LDH + j0 + m) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
-    *reinterpret_cast<f16x4*>(cs.u.t.lo + i * LDH + j0 + m) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
+    merge_offdiag(cs, lane);
+  } else if (pw == 2) {
+    store_p(cs, pa, 1, 0, lane);
+  } else if (pw == 3) {
+    store_p(cs, pa, 0, 0, lane);
+    store_p(cs, pb, 1, 1, lane);
   }
 }
 
