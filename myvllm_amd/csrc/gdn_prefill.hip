@@ -67,6 +67,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const bf16_t* q; const bf16_t* k; const bf16_t* v; const float* g; const void* beta;
@@ -155,16 +156,49 @@ GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
 }
 
+// Maximum over the wave of a non-negative float, on every lane: DPP steps
+// within each 16-lane row (xor 1, xor 2, half-row and row mirrors), then the
+// four row results through scalar registers.  Non-negative floats order like
+// their bit patterns, so the maxima are taken on integers.
+GDN_DEVICE float wave_max_nonneg(float x) {
+  int v = __builtin_bit_cast(int, x);
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const int r = max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+                    max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  return __builtin_bit_cast(float, r);
+}
+
 // Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over the wave's
-// `nt` C tiles (0 when all are zero); the same on every lane.
+// `nt` C tiles (0 when all are zero); the same on every lane.  The per-lane
+// maximum is a tree, so its latency is a few dependent operations.
 GDN_DEVICE int wave_scale_exp(const f32x16* t, int nt) {
-  float m = 0.f;
-  for (int i = 0; i < nt; ++i)
+  float m[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(t[i][j]));
+  for (int j = 0; j < 16; ++j) {
+    m[j] = fabsf(t[0][j]);
+    for (int i = 1; i < nt; ++i) m[j] = fmaxf(m[j], fabsf(t[i][j]));
+  }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  return m > 0.f ? __builtin_amdgcn_frexp_expf(m) - 10 : 0;
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int j = 0; j < w; ++j) m[j] = fmaxf(m[j], m[j + w]);
+  const float mx = wave_max_nonneg(m[0]);
+  return mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 10 : 0;
+}
+
+// Inclusive prefix sum over the 64 lanes (DPP row shifts, then the row
+// broadcasts of the last lane of each row).
+GDN_DEVICE float wave_inclusive_scan(float x) {
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0.f, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return x;
 }
 
 // hi/lo fp16 splits: hi = fp16(x) (round to nearest even), lo = fp16(x - hi).
@@ -187,17 +221,48 @@ GDN_DEVICE void split_pair(float x0, float x1, f16_t& h0, f16_t& h1, f16_t& l0, 
   l1 = l[1];
 }
 
+// Scaled fp16 hi/lo pairs with the mixed-precision FMAs: hi = fp16(x s) and
+// lo = fp16(x s - hi), each rounded once from the exact product, so lo is
+// referenced to exactly the stored hi bits.  A scale per element lets a
+// per-row factor ride along (C-layout neighbours are adjacent rows).
+GDN_DEVICE uint32_t mix_hi_pair(float x0, float s0, float x1, float s1) {
+  uint32_t h;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0 op_sel_hi:[0,0,0]"
+      : "=&v"(h)
+      : "v"(x0), "v"(s0), "v"(x1), "v"(s1));
+  return h;
+}
+GDN_DEVICE uint32_t mix_lo_pair(float x0, float s0, float x1, float s1, uint32_t h) {
+  uint32_t l;
+  asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(l)
+      : "v"(x0), "v"(s0), "v"(x1), "v"(s1), "v"(h));
+  return l;
+}
+
 // split of registers 8h..8h+7 of a C tile, times sc
 GDN_DEVICE void split8(const f32x16& c, int h, float sc, f16x8& hi, f16x8& lo) {
+  uint32_t H[4], L[4];
 #pragma unroll
-  for (int m = 0; m < 8; m += 2) {
-    f16_t a0, a1, b0, b1;
-    split_pair(c[8 * h + m] * sc, c[8 * h + m + 1] * sc, a0, a1, b0, b1);
-    hi[m] = a0;
-    hi[m + 1] = a1;
-    lo[m] = b0;
-    lo[m + 1] = b1;
+  for (int m = 0; m < 4; ++m) {
+    H[m] = mix_hi_pair(c[8 * h + 2 * m], sc, c[8 * h + 2 * m + 1], sc);
+    L[m] = mix_lo_pair(c[8 * h + 2 * m], sc, c[8 * h + 2 * m + 1], sc, H[m]);
   }
+  hi = __builtin_bit_cast(f16x8, (u32x4){H[0], H[1], H[2], H[3]});
+  lo = __builtin_bit_cast(f16x8, (u32x4){L[0], L[1], L[2], L[3]});
+}
+// the same with one factor per register (f[m] scales register 8h + m)
+GDN_DEVICE void split8f(const f32x16& c, int h, const float (&f)[8], f16x8& hi, f16x8& lo) {
+  uint32_t H[4], L[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    H[m] = mix_hi_pair(c[8 * h + 2 * m], f[2 * m], c[8 * h + 2 * m + 1], f[2 * m + 1]);
+    L[m] = mix_lo_pair(c[8 * h + 2 * m], f[2 * m], c[8 * h + 2 * m + 1], f[2 * m + 1], H[m]);
+  }
+  hi = __builtin_bit_cast(f16x8, (u32x4){H[0], H[1], H[2], H[3]});
+  lo = __builtin_bit_cast(f16x8, (u32x4){L[0], L[1], L[2], L[3]});
 }
 template <int N>
 GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
@@ -499,6 +564,7 @@ GDN_DEVICE void store_p(ChunkSlot& cs, const PTile& t, int mt, int nt, int lane)
 // Two producer barriers: after staging, and after the diagonal blocks.
 GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t* count, int32_t& target,
                               int ptid, int pw, int lane) {
+  asm volatile("" : "+v"(lane), "+v"(ptid));  // as in consume_chunk: no hoisted lane masks
   // stage K, Q (to fp16) and V; gamma = in-chunk cumsum of g (wave 4, one token per lane)
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -512,13 +578,9 @@ GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t
     *reinterpret_cast<bf16x8*>(cs.v + row * LDV + 8 * cg) = cl.v[u];
   }
   if (pw == 0) {
-    float gm = cl.g;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(gm, off, 64);
-      if (lane >= off) gm += y;
-    }
-    const float gl = __shfl(gm, 63, 64);  // padded g is 0, so this is gamma at token L-1
+    const float gm = wave_inclusive_scan(cl.g);
+    // padded g is 0, so lane 63 holds gamma at token L-1
+    const float gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gm), 63));
     cs.gam[lane] = gm;
     cs.eg[lane] = __expf(gm);
     cs.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
@@ -555,11 +617,18 @@ GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t
 // ---- state role (waves 0..3) -----------------------------------------------------
 
 // The state products of one chunk on this wave's 32 value columns; writes the
-// chunk's output rows for those columns.
-GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& a, int64_t c0, int L, int h,
-                              int wave, int lane) {
+// chunk's output rows for those columns.  The state is held in units of
+// 2^su (true state = S * 2^su, su wave-uniform): the update rescales S by
+// one factor per chunk and re-bases su on the exponent of V', so no other
+// pass over S is needed for the fp16 splits.
+GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const PrefillArgs& a, int64_t c0, int L,
+                              int h, int wave, int lane) {
+  // Lane-dependent addresses are cheap to recompute; keeping them out of
+  // loop-invariant code motion keeps them out of registers across chunks.
+  asm volatile("" : "+v"(lane));
   const int n = lane & 31, gq = lane >> 5;
   const int col = 32 * wave + n;
+  // X = K S, QS = Q S on the split of S 2^-es (true values: X 2^(es + su))
   const int es = wave_scale_exp(S, 4);
   const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
   f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
@@ -578,8 +647,9 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
     X[0] = mfma32(ak0, slo, X[0]);
     X[1] = mfma32(ak1, slo, X[1]);
   }
-  // R = V - diag(e^gamma) X (X, QS in units of 2^-es; V read transposed: rows are tokens)
-  const float us = __builtin_amdgcn_ldexpf(1.f, es);
+  const int ex = es + su;
+  // R = V - diag(e^gamma) X in true units (V read transposed: rows are tokens)
+  const float xu = __builtin_amdgcn_ldexpf(1.f, ex);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -589,13 +659,14 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
       const bf16_t* p = cs.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
       const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = (float)vv[rr] - egv[rr] * (X[mt][4 * i + rr] * us);
+      for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu), X[mt][4 * i + rr], (float)vv[rr]);
     }
   }
   f32x16* R = X;  // X now holds R
-  const int er = wave_scale_exp(R, 2);
+  // (er >= ex - 100 keeps 2^(ex - er) finite; a smaller R is negligible next to the state)
+  const int er = max(wave_scale_exp(R, 2), ex - 100);
   const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
-  // V' = T' R, in units of 2^-er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
+  // V' = T' R, in units of 2^er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
   f32x16 VN[2] = {zero16(), zero16()};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -620,9 +691,8 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
       VN[1] = mfma32(al1, rhi, VN[1]);
     }
   }
-  // O = scale (diag(e^gamma) Q S + P V')
-  const float ru = __builtin_amdgcn_ldexpf(1.f, er);
-  const float qsu = __builtin_amdgcn_ldexpf(1.f, es - er);
+  // O = scale (diag(e^gamma) Q S + P V') = scale 2^er (diag(e^gamma 2^(ex - er)) QS + P VN)
+  const float qsu = __builtin_amdgcn_ldexpf(1.f, ex - er);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -642,7 +712,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
   }
   // stage this wave's output columns (bf16) in the V tile, then store 16-byte row pieces
   {
-    const float osc = ru * a.scale;
+    const float osc = __builtin_amdgcn_ldexpf(a.scale, er);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -658,29 +728,38 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
             *reinterpret_cast<const bf16x8*>(cs.v + row * LDV + 32 * wave + 8 * cgp);
     }
   }
-  // S = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
+  // S_true' = e^gamma_L S_true + K^T Vd, Vd = diag(e^(gamma_L - gamma)) V' = diag(edec) VN 2^er.
+  // The split operand is Vd 2^-ed with ed = er + evn (max |VN| 2^-evn in [2^9, 2^10),
+  // edec <= 1), and the new state is held in units of 2^ed:
+  //   S' = S e^gamma_L 2^(su - ed) + K^T (Vd 2^-ed).
+  // ed >= ex - 64 keeps S' far inside the fp32 range; evn >= -100 keeps 2^(er - ed) finite.
+  const int ed = max(er + max(wave_scale_exp(VN, 2), -100), ex - 64);
+  const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
+  const float edl = __expf(cs.gam_last);
+  const int dsu = su - ed;
+  if (dsu >= -100 && dsu <= 100) {
+    const float sdec = __builtin_amdgcn_ldexpf(edl, dsu);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4 dv = rows4(cs.edec, 32 * mt, i, lane);
+      for (int j = 0; j < 16; ++j) S[mt][j] *= sdec;
+  } else {  // a factor outside the fp32 range: scale element by element
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) VN[mt][4 * i + rr] *= dv[rr];
-    }
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) S[mt][j] = __builtin_amdgcn_ldexpf(S[mt][j] * edl, dsu);
   }
-  const int ed = wave_scale_exp(VN, 2);
-  const float ds = __builtin_amdgcn_ldexpf(1.f, -ed);
-  // accumulate in units of 2^-(er + ed): S_acc = e^gamma_L S 2^-(er+ed) + K^T Vd_scaled
-  const float sin_ = __expf(cs.gam_last) * __builtin_amdgcn_ldexpf(1.f, -(er + ed));
-  const float sout = __builtin_amdgcn_ldexpf(1.f, er + ed);
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) S[mt][j] *= sin_;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
+    float fd[8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 dv = rows4(cs.edec, 32 * (ks >> 1), 2 * (ks & 1) + i, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) fd[4 * i + rr] = dv[rr] * fdu;
+    }
     f16x8 dhi, dlo;
-    split8(VN[ks >> 1], ks & 1, ds, dhi, dlo);
+    split8f(VN[ks >> 1], ks & 1, fd, dhi, dlo);
     f16x8 akt[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(cs.k, LDK, 32 * mt, 16 * ks, lane);
@@ -689,10 +768,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], const PrefillArgs& 
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dlo, S[mt]);
   }
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) S[mt][j] *= sout;
+  su = ed;
 }
 
 __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
@@ -734,19 +810,21 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     const int col = 32 * wave + n;
     float* Sg = a.state + slot * a.st_slot + h * a.st_head;
     f32x16 S[4];
+    int su = 0;  // state units: true state = S * 2^su
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
-      consume_chunk(sm.slot[c & 1], S, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
+      consume_chunk(sm.slot[c & 1], S, su, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
       __syncthreads();  // slot (c & 1) is free again, slot ((c + 1) & 1) is prepared
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = S[mt][j];
+      for (int j = 0; j < 16; ++j)
+        Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = __builtin_amdgcn_ldexpf(S[mt][j], su);
   } else {
     // ---- producer waves: chunk c + 1 while the state waves work on chunk c
     const int ptid = tid - kRoleThreads, pw = wave - 4;
