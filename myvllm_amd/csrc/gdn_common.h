@@ -115,6 +115,18 @@ GDN_DEVICE float load_scalar_f32(const void* p, int64_t off, int dtype) {
   }
 }
 
+// Raw bits of an fp32 / bf16 / fp16 scalar (no conversion, so a load can stay
+// in flight), and their value.
+GDN_DEVICE uint32_t load_scalar_bits(const void* p, int64_t off, int dtype) {
+  if (dtype == GDN_DTYPE_F32) return reinterpret_cast<const uint32_t*>(p)[off];
+  return reinterpret_cast<const uint16_t*>(p)[off];
+}
+GDN_DEVICE float scalar_bits_f32(uint32_t bits, int dtype) {
+  if (dtype == GDN_DTYPE_BF16) return __builtin_bit_cast(float, bits << 16);
+  if (dtype == GDN_DTYPE_F16) return (float)__builtin_bit_cast(f16_t, (uint16_t)bits);
+  return __builtin_bit_cast(float, bits);
+}
+
 // ---- index tensors (int32 or int64) ----------------------------------------
 GDN_DEVICE int64_t load_index(const void* p, int64_t i, bool is64) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];

@@ -109,7 +109,8 @@ static_assert(2 * 32 * LDS32 * sizeof(float) <= sizeof(f16_t) * C * LDH, "solve 
 
 struct Smem {
   ChunkSlot slot[2];
-  int32_t producer_count;  // producer barrier arrivals
+  int32_t kq_ready;      // arrivals at the producers' first barrier (3 per chunk)
+  int32_t solve_done;    // arrivals at the producers' second barrier (4 per chunk)
   int32_t seq;
 };
 
@@ -365,12 +366,15 @@ GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int
 
 // ---- producer role (waves 4..7) --------------------------------------------------
 
-// Barrier over the four producer waves: an LDS arrival counter that grows by
-// 4 per round.  The wait is bounded so a logic error cannot hang the GPU.
-GDN_DEVICE void producer_sync(int32_t* count, int32_t& target, int lane) {
+// Producer barriers: LDS arrival counters that grow by the number of
+// arriving waves per chunk.  A wave may arrive without waiting (its data is
+// published by the release fence); waits are bounded so a logic error cannot
+// hang the GPU.
+GDN_DEVICE void producer_arrive(int32_t* count, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  target += 4;
   if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+GDN_DEVICE void producer_wait(int32_t* count, int32_t target) {
   for (int spin = 0; spin < kSpinLimit; ++spin) {
     if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
     __builtin_amdgcn_s_sleep(1);
@@ -378,36 +382,90 @@ GDN_DEVICE void producer_sync(int32_t* count, int32_t& target, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// A chunk's inputs in flight in registers.
+// A chunk's inputs in flight in registers.  Waves 4, 5 (solvers of the
+// diagonal blocks of T'): r[0..7] = K fragments of their 32 rows (lane (n, g)
+// holds row 32 pw + n, columns 16 ks + 8 g .. +7), r[8..15] = half of V;
+// g and beta (raw bits) of token `lane`.  Waves 6, 7: r[0..7] = half of K,
+// r[8..15] = half of Q, as 16-byte row pieces.
+//
+// Rows past the chunk's last token are loaded from the last token instead
+// (no divergent loads, so nothing waits on them here): they are inert
+// because their g, beta and e^(gamma_L - gamma) are set to zero, which zeroes
+// their rows and columns of T' and their share of the state update, and
+// their output rows are not stored.
 struct ChunkLoad {
-  bf16x8 k[4], q[4], v[4];
-  float g, b;  // wave 4 only: token `lane`
+  bf16x8 r[16];
+  float g;
+  uint32_t b;
 };
 
-GDN_DEVICE void load_chunk(ChunkLoad& cl, const PrefillArgs& a, const bf16_t* kg, const bf16_t* qg,
-                           const bf16_t* vg, int h, int64_t c0, int64_t e, int ptid, int pw, int lane) {
-  const int64_t rem = e - c0;
+GDN_DEVICE bf16x8 load_row_piece(const bf16_t* base, int64_t stride, int64_t c0, int row, int col, int Lc) {
+  const int rc = row < Lc ? row : Lc - 1;
+  return *reinterpret_cast<const bf16x8*>(base + (c0 + rc) * stride + col);
+}
+
+// Where a (sequence, v-head) reads its chunks from.
+struct ChunkSource {
+  const PrefillArgs* a;
+  const bf16_t* kg;  // k-head base
+  const bf16_t* qg;  // k-head base
+  const bf16_t* vg;  // v-head base
+  int h;             // v-head
+  int64_t e;         // end token of the sequence
+};
+
+enum LoadPart { kLoadKFrag, kLoadVGB, kLoadKQ };
+
+// One part of the loads of the chunk starting at token c0 (see ChunkLoad).
+GDN_DEVICE void load_part(ChunkLoad& cl, const ChunkSource& src, int64_t c0, LoadPart part, int pw, int lane) {
+  const PrefillArgs& a = *src.a;
+  const int64_t rem = src.e - c0;
   const int Lc = (int)(rem < C ? rem : C);
+  const int t2 = ((pw & 1) << 6) | lane;  // thread index within the wave pair
+  if (part == kLoadKFrag) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int vec = ptid + u * kRoleThreads;
-    const int row = vec >> 4, cg = vec & 15;
-    if (row < Lc) {
-      const int64_t t = c0 + row;
-      cl.k[u] = *reinterpret_cast<const bf16x8*>(kg + t * a.k_s0 + 8 * cg);
-      cl.q[u] = *reinterpret_cast<const bf16x8*>(qg + t * a.q_s0 + 8 * cg);
-      cl.v[u] = *reinterpret_cast<const bf16x8*>(vg + t * a.v_s0 + 8 * cg);
-    } else {
+    for (int ks = 0; ks < 8; ++ks)
+      cl.r[ks] = load_row_piece(src.kg, a.k_s0, c0, 32 * pw + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
+  } else if (part == kLoadVGB) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m) { cl.k[u][m] = (bf16_t)0.f; cl.q[u][m] = (bf16_t)0.f; cl.v[u][m] = (bf16_t)0.f; }
+    for (int u = 0; u < 8; ++u) {
+      const int vec = t2 + 128 * u;
+      cl.r[8 + u] = load_row_piece(src.vg, a.v_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
+    }
+    const int64_t t = c0 + (lane < Lc ? lane : Lc - 1);
+    cl.g = a.g[t * a.g_s0 + src.h * a.g_s1];
+    cl.b = load_scalar_bits(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int vec = t2 + 128 * u;
+      cl.r[u] = load_row_piece(src.kg, a.k_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
+      cl.r[8 + u] = load_row_piece(src.qg, a.q_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
     }
   }
-  cl.g = 0.f;
-  cl.b = 0.f;
-  if (pw == 0 && lane < Lc) {
-    cl.g = a.g[(c0 + lane) * a.g_s0 + h * a.g_s1];
-    cl.b = load_scalar_f32(a.beta, (c0 + lane) * a.b_s0 + h * a.b_s1, a.b_dtype);
+}
+
+GDN_DEVICE void load_chunk(ChunkLoad& cl, const ChunkSource& src, int64_t c0, int pw, int lane) {
+  if (pw < 2) {
+    load_part(cl, src, c0, kLoadKFrag, pw, lane);
+    load_part(cl, src, c0, kLoadVGB, pw, lane);
+  } else {
+    load_part(cl, src, c0, kLoadKQ, pw, lane);
   }
+}
+
+// bf16 -> fp16 of 8 values (exact for |x| in the fp16 normal range): the
+// bf16 bits widened to fp32 by a shift or mask, then one packed conversion
+// per pair.
+GDN_DEVICE f16x8 bf16x8_to_f16x8(bf16x8 x) {
+  const u32x4 w = __builtin_bit_cast(u32x4, x);
+  u32x4 o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const f32x2 f = {__builtin_bit_cast(float, w[m] << 16), __builtin_bit_cast(float, w[m] & 0xffff0000u)};
+    o[m] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+  }
+  return __builtin_bit_cast(f16x8, o);
 }
 
 // Gram tile (mt, nt) of rows of M1 against rows of M2 (K = 128): C layout,
@@ -421,14 +479,21 @@ GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, in
 }
 
 // Diagonal block `blk` of T': A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
-// from the kk^T tile, solved in fp32 in the wave's scratch block (16x16
+// from the kk^T tile (K fragments in registers), solved in fp32 in the wave's scratch block (16x16
 // substitution + one MFMA merge), then T'_bb = T_bb diag(beta) written as
 // fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's LDS
 // accesses complete in program order.
-GDN_DEVICE void solve_diag_block(ChunkSlot& cs, int blk, int lane) {
+// kk^T of a diagonal block's rows from the register fragments (bf16 holds k exactly)
+GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[16]) {
+  f32x16 G = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KD / 16; ++ks) G = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], kf[ks], G, 0, 0, 0);
+  return G;
+}
+
+GDN_DEVICE void solve_diag_block(ChunkSlot& cs, int blk, const f32x16& G, int lane) {
   const int n = lane & 31, gq = lane >> 5, o = 32 * blk;
   float* A = reinterpret_cast<float*>(cs.p) + blk * 32 * LDS32;
-  const f32x16 G = gram_tile(cs.k, cs.k, blk, blk, lane);
   const float gj = cs.gam[o + n];
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
@@ -561,48 +626,61 @@ GDN_DEVICE void store_p(ChunkSlot& cs, const PTile& t, int mt, int nt, int lane)
 }
 
 // Everything of a chunk that does not depend on the state, written to slot cs.
-// Two producer barriers: after staging, and after the diagonal blocks.
-GDN_DEVICE void prepare_chunk(ChunkSlot& cs, const ChunkLoad& cl, int L, int32_t* count, int32_t& target,
-                              int ptid, int pw, int lane) {
-  asm volatile("" : "+v"(lane), "+v"(ptid));  // as in consume_chunk: no hoisted lane masks
-  // stage K, Q (to fp16) and V; gamma = in-chunk cumsum of g (wave 4, one token per lane)
+//  * waves 4, 5: stage V and the decay vectors (identical values from both),
+//    then solve their diagonal block of T' from K fragments in registers --
+//    without waiting for anyone;
+//  * waves 6, 7: stage K and Q (fp16), wait for each other and for wave 4's
+//    decay vectors, then form B_10 and the P tiles;
+//  * after a barrier of all four: wave 4 forms T'_10, waves 6, 7 store P.
+GDN_DEVICE void prepare_chunk(ChunkSlot& cs, ChunkLoad& cl, int L, const ChunkSource& src, int64_t next_c0,
+                              bool has_next, Smem& sm, int32_t& t_kq, int32_t& t_solve, int pw, int lane) {
+  asm volatile("" : "+v"(lane));  // as in consume_chunk: no hoisted lane masks
+  const int t2 = ((pw & 1) << 6) | lane;
+  PTile pa, pb;
+  if (pw < 2) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int vec = ptid + u * kRoleThreads;
-    const int row = vec >> 4, cg = vec & 15;
-    f16x8 k16, q16;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) { k16[m] = (f16_t)(float)cl.k[u][m]; q16[m] = (f16_t)(float)cl.q[u][m]; }
-    *reinterpret_cast<f16x8*>(cs.k + row * LDK + 8 * cg) = k16;
-    *reinterpret_cast<f16x8*>(cs.q + row * LDK + 8 * cg) = q16;
-    *reinterpret_cast<bf16x8*>(cs.v + row * LDV + 8 * cg) = cl.v[u];
-  }
-  if (pw == 0) {
-    const float gm = wave_inclusive_scan(cl.g);
+    for (int u = 0; u < 8; ++u) {
+      const int vec = t2 + 128 * u;
+      *reinterpret_cast<bf16x8*>(cs.v + (vec >> 4) * LDV + 8 * (vec & 15)) = cl.r[8 + u];
+    }
+    // gamma = in-chunk cumsum of g, one token per lane
+    const float gm = wave_inclusive_scan(lane < L ? cl.g : 0.f);
     // padded g is 0, so lane 63 holds gamma at token L-1
     const float gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gm), 63));
     cs.gam[lane] = gm;
     cs.eg[lane] = __expf(gm);
     cs.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
-    cs.beta[lane] = cl.b;
+    cs.beta[lane] = lane < L ? scalar_bits_f32(cl.b, src.a->b_dtype) : 0.f;
     if (lane == 0) cs.gam_last = gl;
-  }
-  producer_sync(count, target, lane);
-
-  // waves 4, 5: diagonal blocks of T' (scratch in the P region); wave 6: B_10
-  // and P tile (1,0); wave 7: P tiles (0,0), (1,1).  P stays in registers
-  // until the scratch is free.
-  PTile pa, pb;
-  if (pw < 2) {
-    solve_diag_block(cs, pw, lane);
-  } else if (pw == 2) {
-    b10_block(cs, lane);
-    pa = qk_tile(cs, 1, 0, lane);
+    if (pw == 0) producer_arrive(&sm.kq_ready, lane);
+    // the next chunk's loads go out as soon as their registers are free
+    if (has_next) load_part(cl, src, next_c0, kLoadVGB, pw, lane);
+    const f32x16 G = gram_regs(cl.r);
+    if (has_next) load_part(cl, src, next_c0, kLoadKFrag, pw, lane);
+    solve_diag_block(cs, pw, G, lane);
   } else {
-    pa = qk_tile(cs, 0, 0, lane);
-    pb = qk_tile(cs, 1, 1, lane);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int vec = t2 + 128 * u;
+      const int off = (vec >> 4) * LDK + 8 * (vec & 15);
+      *reinterpret_cast<f16x8*>(cs.k + off) = bf16x8_to_f16x8(cl.r[u]);
+      *reinterpret_cast<f16x8*>(cs.q + off) = bf16x8_to_f16x8(cl.r[8 + u]);
+    }
+    if (has_next) load_part(cl, src, next_c0, kLoadKQ, pw, lane);
+    producer_arrive(&sm.kq_ready, lane);
+    t_kq += 3;
+    producer_wait(&sm.kq_ready, t_kq);
+    if (pw == 2) {
+      b10_block(cs, lane);
+      pa = qk_tile(cs, 1, 0, lane);
+    } else {
+      pa = qk_tile(cs, 0, 0, lane);
+      pb = qk_tile(cs, 1, 1, lane);
+    }
   }
-  producer_sync(count, target, lane);
+  producer_arrive(&sm.solve_done, lane);
+  t_solve += 4;
+  producer_wait(&sm.solve_done, t_solve);
 
   if (pw == 0) {
     merge_offdiag(cs, lane);
@@ -783,7 +861,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   const int64_t bid = blockIdx.x;
   const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
   if (work >= a.nseq * a.Hv) return;
-  if (tid == 0) sm.producer_count = 0;
+  if (tid == 0) {
+    sm.kq_ready = 0;
+    sm.solve_done = 0;
+  }
   const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
   const int h = (int)(work % a.Hv);
   const int kh = h / a.r;
@@ -827,20 +908,20 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
         Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = __builtin_amdgcn_ldexpf(S[mt][j], su);
   } else {
     // ---- producer waves: chunk c + 1 while the state waves work on chunk c
-    const int ptid = tid - kRoleThreads, pw = wave - 4;
+    const int pw = wave - 4;
     const bf16_t* qg = a.q + kh * a.q_s1;
     const bf16_t* kg = a.k + kh * a.k_s1;
     const bf16_t* vg = a.v + h * a.v_s1;
-    int32_t target = 0;
+    int32_t t_kq = 0, t_solve = 0;
+    const ChunkSource src = {&a, kg, qg, vg, h, e};
     ChunkLoad cl;
-    load_chunk(cl, a, kg, qg, vg, h, s, e, ptid, pw, lane);
-    prepare_chunk(sm.slot[0], cl, chunk_len(0), &sm.producer_count, target, ptid, pw, lane);
-    if (nc > 1) load_chunk(cl, a, kg, qg, vg, h, s + C, e, ptid, pw, lane);
+    load_chunk(cl, src, s, pw, lane);
+    prepare_chunk(sm.slot[0], cl, chunk_len(0), src, s + C, nc > 1, sm, t_kq, t_solve, pw, lane);
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
       if (c + 1 < nc) {
-        prepare_chunk(sm.slot[(c + 1) & 1], cl, chunk_len(c + 1), &sm.producer_count, target, ptid, pw, lane);
-        if (c + 2 < nc) load_chunk(cl, a, kg, qg, vg, h, s + (int64_t)(c + 2) * C, e, ptid, pw, lane);
+        prepare_chunk(sm.slot[(c + 1) & 1], cl, chunk_len(c + 1), src, s + (int64_t)(c + 2) * C, c + 2 < nc, sm, t_kq,
+                      t_solve, pw, lane);
       }
       __syncthreads();
     }
