@@ -132,6 +132,11 @@ int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* 
   // index ranges
   if (prefill) {
     if (idx->shape[0] * Hv > kMaxGrid || T > kMaxGrid) return GDN_ERR_RANGE;
+    // the prefill kernel addresses the rows of a 64-token chunk with 32-bit offsets
+    const int64_t kMaxTokenStride = int64_t(1) << 24;
+    if (q->stride[0] > kMaxTokenStride || k->stride[0] > kMaxTokenStride || v->stride[0] > kMaxTokenStride ||
+        out->stride[0] > kMaxTokenStride)
+      return GDN_ERR_RANGE;
   } else {
     if (T * Hv > kMaxGrid) return GDN_ERR_RANGE;
   }

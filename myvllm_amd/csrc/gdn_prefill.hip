@@ -399,9 +399,12 @@ struct ChunkLoad {
   uint32_t b;
 };
 
-GDN_DEVICE bf16x8 load_row_piece(const bf16_t* base, int64_t stride, int64_t c0, int row, int col, int Lc) {
-  const int rc = row < Lc ? row : Lc - 1;
-  return *reinterpret_cast<const bf16x8*>(base + (c0 + rc) * stride + col);
+// 16 bytes of row `row` of a chunk (uniform base pointer of the chunk's first
+// token + a 32-bit lane offset; the host guarantees 64 token strides fit).
+GDN_DEVICE bf16x8 load_row_piece(const bf16_t* chunk_base, uint32_t stride, int row, int col, int Lc) {
+  const uint32_t rc = (uint32_t)(row < Lc ? row : Lc - 1);
+  const uint32_t byte_off = (rc * stride + (uint32_t)col) * (uint32_t)sizeof(bf16_t);
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(chunk_base) + byte_off);
 }
 
 // Where a (sequence, v-head) reads its chunks from.
@@ -423,24 +426,28 @@ GDN_DEVICE void load_part(ChunkLoad& cl, const ChunkSource& src, int64_t c0, Loa
   const int Lc = (int)(rem < C ? rem : C);
   const int t2 = ((pw & 1) << 6) | lane;  // thread index within the wave pair
   if (part == kLoadKFrag) {
+    const bf16_t* kb = src.kg + c0 * a.k_s0;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      cl.r[ks] = load_row_piece(src.kg, a.k_s0, c0, 32 * pw + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
+      cl.r[ks] = load_row_piece(kb, (uint32_t)a.k_s0, 32 * pw + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
   } else if (part == kLoadVGB) {
+    const bf16_t* vb = src.vg + c0 * a.v_s0;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int vec = t2 + 128 * u;
-      cl.r[8 + u] = load_row_piece(src.vg, a.v_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
+      cl.r[8 + u] = load_row_piece(vb, (uint32_t)a.v_s0, vec >> 4, 8 * (vec & 15), Lc);
     }
     const int64_t t = c0 + (lane < Lc ? lane : Lc - 1);
     cl.g = a.g[t * a.g_s0 + src.h * a.g_s1];
     cl.b = load_scalar_bits(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
   } else {
+    const bf16_t* kb = src.kg + c0 * a.k_s0;
+    const bf16_t* qb = src.qg + c0 * a.q_s0;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int vec = t2 + 128 * u;
-      cl.r[u] = load_row_piece(src.kg, a.k_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
-      cl.r[8 + u] = load_row_piece(src.qg, a.q_s0, c0, vec >> 4, 8 * (vec & 15), Lc);
+      cl.r[u] = load_row_piece(kb, (uint32_t)a.k_s0, vec >> 4, 8 * (vec & 15), Lc);
+      cl.r[8 + u] = load_row_piece(qb, (uint32_t)a.q_s0, vec >> 4, 8 * (vec & 15), Lc);
     }
   }
 }
@@ -798,11 +805,12 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
         const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
         cs.v[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
       }
+    bf16_t* ob = a.out + c0 * a.o_s0 + h * a.o_s1 + 32 * wave;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int row = 16 * u + (lane >> 2), cgp = lane & 3;
       if (row < L)
-        *reinterpret_cast<bf16x8*>(a.out + (c0 + row) * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * cgp) =
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<char*>(ob) + ((uint32_t)row * (uint32_t)a.o_s0 + 8u * cgp) * 2u) =
             *reinterpret_cast<const bf16x8*>(cs.v + row * LDV + 32 * wave + 8 * cgp);
     }
   }
