@@ -115,16 +115,28 @@ GDN_DEVICE float load_scalar_f32(const void* p, int64_t off, int dtype) {
   }
 }
 
-// Raw bits of an fp32 / bf16 / fp16 scalar (no conversion, so a load can stay
-// in flight), and their value.
-GDN_DEVICE uint32_t load_scalar_bits(const void* p, int64_t off, int dtype) {
-  if (dtype == GDN_DTYPE_F32) return reinterpret_cast<const uint32_t*>(p)[off];
-  return reinterpret_cast<const uint16_t*>(p)[off];
+// An fp32 / bf16 / fp16 scalar as two raw 16-bit halves, loaded without a
+// branch on the dtype (for 16-bit types both halves are the element), and
+// its value.  Keeping the load unconditional and the conversion separate
+// lets the caller convert only after its other loads are in flight: a load
+// inside a branch, or a conversion right after the load, makes the wave wait
+// for every earlier vector load (they complete in order).
+struct ScalarRaw {
+  uint32_t lo, hi;
+};
+GDN_DEVICE ScalarRaw load_scalar_raw(const void* p, int64_t off, int dtype) {
+  const int shift = dtype == GDN_DTYPE_F32 ? 2 : 1;  // log2 of the element size
+  const uint16_t* e = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p) + (off << shift));
+  const int second = shift - 1;  // 1 for fp32 (the high half), 0 otherwise
+  ScalarRaw r;
+  r.lo = e[0];
+  r.hi = e[second];
+  return r;
 }
-GDN_DEVICE float scalar_bits_f32(uint32_t bits, int dtype) {
-  if (dtype == GDN_DTYPE_BF16) return __builtin_bit_cast(float, bits << 16);
-  if (dtype == GDN_DTYPE_F16) return (float)__builtin_bit_cast(f16_t, (uint16_t)bits);
-  return __builtin_bit_cast(float, bits);
+GDN_DEVICE float scalar_raw_f32(ScalarRaw r, int dtype) {
+  if (dtype == GDN_DTYPE_BF16) return __builtin_bit_cast(float, r.lo << 16);
+  if (dtype == GDN_DTYPE_F16) return (float)__builtin_bit_cast(f16_t, (uint16_t)r.lo);
+  return __builtin_bit_cast(float, (r.hi << 16) | r.lo);
 }
 
 // ---- index tensors (int32 or int64) ----------------------------------------

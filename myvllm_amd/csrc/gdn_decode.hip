@@ -3,12 +3,13 @@
 // Replaces the Triton kernel _fused_recurrent_gdn
 // (ops/gated_delta_rule/fused_recurrent_gdn.py:6-102 in yuyifanbupt/myvllm),
 // which tiles the fp32 state as 128x8 slabs (32 contiguous bytes per row).
-// Here one 256-thread workgroup owns the whole K x V fp32 state of one
+// Here one 1024-thread workgroup owns the whole K x V fp32 state of one
 // (sequence, v-head): every thread streams V/4-wide rows with 16-byte loads
 // (a wave reads 1 KiB contiguous per instruction), both reductions over K
 // (k^T S and q^T S) are done in the same pass, and the updated state is
 // written back in place, so the state crosses HBM exactly once each way
 // (non-temporal loads and stores: nothing of it is reused by this launch).
+// The kernel template takes NH heads per workgroup; the launcher uses one.
 //
 // Math per (b, h), with S decayed first (fused_recurrent_gdn.py:96-99):
 //   kS = k^T S, qS = (scale q)^T S                  (old S)
@@ -31,9 +32,11 @@ struct RecurrentArgs {
   bool idx64;
 };
 
-constexpr int kThreads = 256;
+// 16 waves, 4 state rows each: the shortest load-to-store span per workgroup
+// (measured against 256 / 512 threads and two heads per workgroup).
+constexpr int kThreads = 1024;
 
-template <typename TIn, int K, int V>
+template <typename TIn, int K, int V, int NH>
 __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentArgs a) {
   constexpr int CG = V / 4;           // float4 column groups per row
   constexpr int RG = kThreads / CG;   // row groups
@@ -41,112 +44,171 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
   constexpr int WAVES = kThreads / 64;
   static_assert(kThreads % CG == 0 && K % RG == 0 && 64 % CG == 0, "shape");
 
-  __shared__ float sq[K], sk[K], sv[V];
-  __shared__ float red[WAVES][CG][9];
+  static_assert(CG * NH <= kThreads, "finishers");
+  __shared__ float sq[NH][K], sk[NH][K], sv[NH][V];
+  __shared__ float red[WAVES][NH][9][CG];
+  __shared__ f32x4 sd[NH][CG];
 
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.x / a.Hv;
-  const int h = blockIdx.x % a.Hv;
-  const int kh = h / a.r;
+  const int hpb = a.Hv / NH;  // workgroups per sequence
+  const int64_t b = blockIdx.x / hpb;
+  const int h0 = (int)(blockIdx.x % hpb) * NH;
   const int c4 = tid % CG;
   const int r0 = tid / CG;
 
   const int64_t slot = load_index(a.idx, b, a.idx64);
-  TIn* o = reinterpret_cast<TIn*>(a.out) + b * a.o_s0 + h * a.o_s1;
   if (slot < 0 || slot >= a.num_slots) {  // padding sequence: zero output, state untouched
-    if (tid < V) o[tid] = from_f32<TIn>(0.0f);
+#pragma unroll
+    for (int n = 0; n < NH; ++n)
+      if (tid < V) reinterpret_cast<TIn*>(a.out)[b * a.o_s0 + (h0 + n) * a.o_s1 + tid] = from_f32<TIn>(0.0f);
     return;
   }
 
-  float* S = a.state + slot * a.st_slot + h * a.st_head;
-  f32x4 s[NI];
+  // The small inputs are loaded first, unconditionally (clamped indices) and
+  // without dtype branches, and converted only after the state loads are in
+  // flight: a conversion right after its load, or a load inside a branch,
+  // would wait for every earlier load (vector loads complete in order).
+  const int kj = tid < K ? tid : 0;
+  const int vj = tid >= kThreads - V ? tid - (kThreads - V) : 0;
+  TIn qr[NH], kr[NH], vr[NH];
+  ScalarRaw graw[NH], braw[NH];
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
-    s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4));
+  for (int n = 0; n < NH; ++n) {
+    const int h = h0 + n, kh = h / a.r;
+    qr[n] = reinterpret_cast<const TIn*>(a.q)[b * a.q_s0 + kh * a.q_s1 + kj];
+    kr[n] = reinterpret_cast<const TIn*>(a.k)[b * a.k_s0 + kh * a.k_s1 + kj];
+    vr[n] = reinterpret_cast<const TIn*>(a.v)[b * a.v_s0 + h * a.v_s1 + vj];
+    graw[n] = load_scalar_raw(a.g, b * a.g_s0 + h * a.g_s1, a.g_dtype);
+    braw[n] = load_scalar_raw(a.beta, b * a.b_s0 + h * a.b_s1, a.b_dtype);
+  }
 
-  if (tid < K) {
-    sq[tid] = to_f32(reinterpret_cast<const TIn*>(a.q)[b * a.q_s0 + kh * a.q_s1 + tid]) * a.scale;
-    sk[tid] = to_f32(reinterpret_cast<const TIn*>(a.k)[b * a.k_s0 + kh * a.k_s1 + tid]);
+  float* S[NH];
+  f32x4 s[NH][NI];
+#pragma unroll
+  for (int n = 0; n < NH; ++n) {
+    S[n] = a.state + slot * a.st_slot + (h0 + n) * a.st_head;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      s[n][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S[n] + (int64_t)(r0 + RG * i) * V + 4 * c4));
   }
-  if (tid >= kThreads - V) {
-    const int j = tid - (kThreads - V);
-    sv[j] = to_f32(reinterpret_cast<const TIn*>(a.v)[b * a.v_s0 + h * a.v_s1 + j]);
+
+  float g[NH], beta[NH];
+#pragma unroll
+  for (int n = 0; n < NH; ++n) {
+    if (tid < K) {
+      sq[n][tid] = to_f32(qr[n]) * a.scale;
+      sk[n][tid] = to_f32(kr[n]);
+    }
+    if (tid >= kThreads - V) sv[n][vj] = to_f32(vr[n]);
+    g[n] = scalar_raw_f32(graw[n], a.g_dtype);
+    beta[n] = scalar_raw_f32(braw[n], a.b_dtype);
   }
-  const float g = load_scalar_f32(a.g, b * a.g_s0 + h * a.g_s1, a.g_dtype);
-  const float beta = load_scalar_f32(a.beta, b * a.b_s0 + h * a.b_s1, a.b_dtype);
   __syncthreads();
 
   // partial reductions over this thread's rows
-  float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f}, qk = 0.f;
+  float pk[NH][4], pq[NH][4], qk[NH];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const float kv = sk[r0 + RG * i];
-    const float qv = sq[r0 + RG * i];
+  for (int n = 0; n < NH; ++n) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pk[j] = fmaf(kv, s[i][j], pk[j]);
-      pq[j] = fmaf(qv, s[i][j], pq[j]);
+    for (int j = 0; j < 4; ++j) pk[n][j] = pq[n][j] = 0.f;
+    qk[n] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float kv = sk[n][r0 + RG * i];
+      const float qv = sq[n][r0 + RG * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pk[n][j] = fmaf(kv, s[n][i][j], pk[n][j]);
+        pq[n][j] = fmaf(qv, s[n][i][j], pq[n][j]);
+      }
+      qk[n] = fmaf(qv, kv, qk[n]);
     }
-    qk = fmaf(qv, kv, qk);
   }
   // reduce over row groups inside the wave (lanes with equal c4 differ by CG)
 #pragma unroll
   for (int off = CG; off < 64; off <<= 1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pk[j] += __shfl_xor(pk[j], off, 64);
-      pq[j] += __shfl_xor(pq[j], off, 64);
+    for (int n = 0; n < NH; ++n) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pk[n][j] += __shfl_xor(pk[n][j], off, 64);
+        pq[n][j] += __shfl_xor(pq[n][j], off, 64);
+      }
+      qk[n] += __shfl_xor(qk[n], off, 64);
     }
-    qk += __shfl_xor(qk, off, 64);
   }
   const int wave = tid >> 6;
   if ((tid & 63) < CG) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      red[wave][c4][j] = pk[j];
-      red[wave][c4][4 + j] = pq[j];
+    for (int n = 0; n < NH; ++n) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[wave][n][j][c4] = pk[n][j];
+        red[wave][n][4 + j][c4] = pq[n][j];
+      }
+      red[wave][n][8][c4] = qk[n];
     }
-    red[wave][c4][8] = qk;
   }
   __syncthreads();
-  float kS[4] = {0.f, 0.f, 0.f, 0.f}, qS[4] = {0.f, 0.f, 0.f, 0.f};
-  qk = 0.f;
+
+  // CG x NH finisher threads sum the waves' partials, form d and the output,
+  // and hand d back through LDS (every thread reading all partials would
+  // multiply the LDS traffic by the number of row groups).
+  if (tid < CG * NH) {
+    const int n = tid / CG, c = tid % CG;
+    float kS[4] = {0.f, 0.f, 0.f, 0.f}, qS[4] = {0.f, 0.f, 0.f, 0.f}, qkn = 0.f;
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      kS[j] += red[w][c4][j];
-      qS[j] += red[w][c4][4 + j];
+      for (int j = 0; j < 4; ++j) {
+        kS[j] += red[w][n][j][c];
+        qS[j] += red[w][n][4 + j][c];
+      }
+      qkn += red[w][n][8][c];
     }
-    qk += red[w][c4][8];
+    float gn = g[0], bn = beta[0];
+#pragma unroll
+    for (int m = 1; m < NH; ++m)
+      if (n == m) {
+        gn = g[m];
+        bn = beta[m];
+      }
+    const float eg = __expf(gn);
+    f32x4 d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = bn * (sv[n][4 * c + j] - eg * kS[j]);
+    sd[n][c] = d;
+    TIn* o = reinterpret_cast<TIn*>(a.out) + b * a.o_s0 + (h0 + n) * a.o_s1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[4 * c + j] = from_f32<TIn>(fmaf(eg, qS[j], qkn * d[j]));
   }
-
-  const float eg = __expf(g);
-  float d[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) d[j] = beta * (sv[4 * c4 + j] - eg * kS[j]);
+  __syncthreads();
 
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const float kv = sk[r0 + RG * i];
-    f32x4 t;
+  for (int n = 0; n < NH; ++n) {
+    const float eg = __expf(g[n]);
+    const f32x4 d = sd[n][c4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) t[j] = fmaf(eg, s[i][j], kv * d[j]);
-    __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(S + (int64_t)(r0 + RG * i) * V + 4 * c4));
-  }
-  if (r0 == 0) {
+    for (int i = 0; i < NI; ++i) {
+      const float kv = sk[n][r0 + RG * i];
+      f32x4 t;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[4 * c4 + j] = from_f32<TIn>(fmaf(eg, qS[j], qk * d[j]));
+      for (int j = 0; j < 4; ++j) t[j] = fmaf(eg, s[n][i][j], kv * d[j]);
+      __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(S[n] + (int64_t)(r0 + RG * i) * V + 4 * c4));
+    }
   }
 }
 
-template <typename TIn>
-hipError_t launch_dims(const RecurrentArgs& a, int K, int V, int64_t nblocks, hipStream_t st) {
-  if (K == 128 && V == 128)
-    gdn_recurrent_step_kernel<TIn, 128, 128><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
-  else
-    gdn_recurrent_step_kernel<TIn, 64, 64><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
+template <typename TIn, int K, int V>
+hipError_t launch_heads(const RecurrentArgs& a, int64_t nitems, hipStream_t st) {
+  gdn_recurrent_step_kernel<TIn, K, V, 1><<<dim3((unsigned)nitems), dim3(kThreads), 0, st>>>(a);
   return hipGetLastError();
+}
+
+template <typename TIn>
+hipError_t launch_dims(const RecurrentArgs& a, int K, int V, int64_t nitems, hipStream_t st) {
+  if (K == 128 && V == 128) return launch_heads<TIn, 128, 128>(a, nitems, st);
+  return launch_heads<TIn, 64, 64>(a, nitems, st);
 }
 
 }  // namespace

@@ -396,7 +396,7 @@ GDN_DEVICE void producer_wait(int32_t* count, int32_t target) {
 struct ChunkLoad {
   bf16x8 r[16];
   float g;
-  uint32_t b;
+  ScalarRaw b;
 };
 
 // 16 bytes of row `row` of a chunk (uniform base pointer of the chunk's first
@@ -439,7 +439,7 @@ GDN_DEVICE void load_part(ChunkLoad& cl, const ChunkSource& src, int64_t c0, Loa
     }
     const int64_t t = c0 + (lane < Lc ? lane : Lc - 1);
     cl.g = a.g[t * a.g_s0 + src.h * a.g_s1];
-    cl.b = load_scalar_bits(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
+    cl.b = load_scalar_raw(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
   } else {
     const bf16_t* kb = src.kg + c0 * a.k_s0;
     const bf16_t* qb = src.qg + c0 * a.q_s0;
@@ -657,7 +657,7 @@ GDN_DEVICE void prepare_chunk(ChunkSlot& cs, ChunkLoad& cl, int L, const ChunkSo
     cs.gam[lane] = gm;
     cs.eg[lane] = __expf(gm);
     cs.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
-    cs.beta[lane] = lane < L ? scalar_bits_f32(cl.b, src.a->b_dtype) : 0.f;
+    cs.beta[lane] = lane < L ? scalar_raw_f32(cl.b, src.a->b_dtype) : 0.f;
     if (lane == 0) cs.gam_last = gl;
     if (pw == 0) producer_arrive(&sm.kq_ready, lane);
     // the next chunk's loads go out as soon as their registers are free

@@ -82,3 +82,12 @@ def test_decode_batch256_full(dev):
     untouched = torch.ones(1024, dtype=torch.bool)
     untouched[sel] = False
     assert torch.equal(st[untouched], case.state[untouched])
+
+
+@pytest.mark.parametrize("Hk, Hv", [(1, 3), (2, 2), (3, 6)])
+def test_decode_head_pairing(dev, Hk, Hv):
+    """Odd Hv (one v-head per workgroup) and GVA ratios 1 and 2 with paired v-heads."""
+    case = decode_case(B=5, num_slots=7, seed=11, Hk=Hk, Hv=Hv)
+    o, st, o_ref, st_ref = _run(case, dev)
+    assert_out_close(o, o_ref)
+    assert_state_close(st, st_ref)
