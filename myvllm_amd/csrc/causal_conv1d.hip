@@ -6,13 +6,13 @@
 // yuyifanbupt/myvllm).  Both are HBM-streaming kernels: each thread owns 8
 // consecutive channels (one 16-byte bf16 vector) and walks tokens, keeping
 // the W-1 previous inputs in registers, so x is read once (plus a W-1 row
-// halo per 32-token tile) and y written once, fully coalesced.
+// halo per 64-token tile) and y written once, fully coalesced.
 //
-// Prefill tiling: each sequence is cut into 32-token tiles; blockIdx.x is a
+// Prefill tiling: each sequence is cut into 64-token tiles; blockIdx.x is a
 // linear tile id resolved to (sequence, tile) on the device, so no host sync
 // is needed (the reference calls .tolist() on cu_seqlens, ops/causal_conv1d.py:230).
 // Only a sequence's first tile reads its old conv state (a later tile's
-// window starts >= 32 > W-1 tokens into the sequence), and that same tile
+// window starts >= 64 > W-1 tokens into the sequence), and that same tile
 // writes the new state, so the read-before-write order on a slot is the
 // program order of one thread.
 #include "gdn_common.h"
@@ -20,7 +20,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTile = 32;  // tokens per prefill tile (>= W - 1, see the state-ownership note)
+constexpr int kTile = 64;  // tokens per prefill tile (>= W - 1, see the state-ownership note)
 constexpr int kCh = 8;     // channels per thread
 constexpr int kBatch = 8;  // token rows loaded together
 
@@ -31,23 +31,55 @@ struct ConvArgs {
   bool idx64, cu64;
 };
 
-template <typename TW>
-GDN_DEVICE void load_weights(const ConvArgs& a, int64_t d0, int W, float (*wr)[kCh]) {
-  const TW* w = reinterpret_cast<const TW*>(a.w);
+// Taps are held pre-multiplied by -log2(e), so a convolution gives
+// a = -log2(e) * acc directly, and
+//   silu(acc) = acc / (1 + e^-acc) = a / (-log2(e) * (1 + 2^a)),
+// one exp2, one fma, one reciprocal and one multiply per element.
+constexpr float kNegLog2e = -1.4426950408889634f;
+GDN_DEVICE float silu_from_scaled(float a) {
+  return a * __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(a), kNegLog2e, kNegLog2e));
+}
+GDN_DEVICE void scale_taps(float (*wr)[kCh], int W) {
   for (int j = 0; j < W; ++j)
 #pragma unroll
-    for (int c = 0; c < kCh; ++c) wr[j][c] = to_f32(w[(d0 + c) * a.w_s0 + j * a.w_s1]);
+    for (int c = 0; c < kCh; ++c) wr[j][c] *= kNegLog2e;
 }
 
-template <typename TX, typename TW, typename TS, int W>
-__global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs a) {
-  __shared__ int64_t lds[8];
-  int64_t seq, tile;
-  find_seq_tile<kThreads>(a.cu, a.cu64, a.nseq, a.T, kTile, blockIdx.x, seq, tile, lds);
-  if (seq < 0) return;
-  const int64_t d0 = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * kCh;
-  if (d0 >= a.D) return;
+// The taps of this thread's 8 channels.  A contiguous, 16-byte aligned
+// (D, W) weight puts them in 8 W consecutive elements, read as 16-byte
+// vectors; any other layout is read element by element.
+template <typename TW, int W>
+GDN_DEVICE void load_weights(const ConvArgs& a, int64_t d0, float (*wr)[kCh]) {
+  const TW* w = reinterpret_cast<const TW*>(a.w);
+  if (a.w_s1 == 1 && a.w_s0 == W && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+    constexpr int kPer = 16 / (int)sizeof(TW);  // elements per 16-byte vector
+    constexpr int kVec = kCh * W / kPer;
+    static_assert((kCh * W) % kPer == 0, "whole vectors");
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v* p = reinterpret_cast<const u32x4v*>(w + d0 * W);
+    TW e[kCh * W];
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      const u32x4v v = p[i];
+      const TW* ev = reinterpret_cast<const TW*>(&v);
+#pragma unroll
+      for (int m = 0; m < kPer; ++m) e[i * kPer + m] = ev[m];
+    }
+#pragma unroll
+    for (int c = 0; c < kCh; ++c)
+#pragma unroll
+      for (int j = 0; j < W; ++j) wr[j][c] = to_f32(e[c * W + j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < W; ++j)
+#pragma unroll
+      for (int c = 0; c < kCh; ++c) wr[j][c] = to_f32(w[(d0 + c) * a.w_s0 + j * a.w_s1]);
+  }
+}
 
+// One tile (up to kTile tokens of one sequence) for this thread's 8 channels.
+template <typename TX, typename TS, int W>
+GDN_DEVICE void conv_tile(const ConvArgs& a, int64_t seq, int64_t tile, int64_t d0, const float (*wr)[kCh]) {
   int64_t s, e;
   seq_range(a.cu, a.cu64, seq, a.T, s, e);
   const int64_t slot = load_index(a.idx, seq, a.idx64);
@@ -63,9 +95,6 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
     return;
   }
 
-  float wr[W][kCh];
-  load_weights<TW>(a, d0, W, wr);
-
   // window[m] = input at position t - (W-1) + m for the next token t
   float win[W - 1][kCh];
   TS* st = reinterpret_cast<TS*>(a.state) + slot * a.st_s0 + d0;
@@ -79,44 +108,55 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
     }
   }
 
-  // token rows in batches of kBatch, the next batch's loads in flight while
-  // the current one is computed (two statically named buffers)
+  // The tile's kTile token rows in batches of kBatch, the next batch's loads in
+  // flight while the current one is computed (two statically named buffers).
+  // The tile is unrolled completely, so the window rotates by register
+  // renaming.  Rows past the sequence end are loaded from its last row and
+  // computed like the others (only their stores are skipped): no branch and
+  // no wait on the loads.  Rows are addressed from the tile's first row with
+  // 32-bit offsets (kTile * stride fits; checked on the host).
+  const TX* xt = x + t0 * a.x_s0 + d0;
+  TX* ot = out + t0 * a.o_s0 + d0;
+  const int nt = (int)(t1 - t0);  // valid rows of this tile, 1..kTile
+  const uint32_t xs = (uint32_t)a.x_s0, os = (uint32_t)a.o_s0;
   Raw8<TX> xa[kBatch], xb[kBatch];
-  auto load_batch = [&](int64_t tb, Raw8<TX>* dst) {
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (tb + u < t1) dst[u].load(x + (tb + u) * a.x_s0 + d0);
-  };
-  auto run_batch = [&](int64_t tb, const Raw8<TX>* raw) {
+  auto load_batch = [&](int r0, Raw8<TX>* dst) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      if (tb + u < t1) {
-        float xr[kCh], y[kCh];
-        raw[u].expand(xr);
-#pragma unroll
-        for (int c = 0; c < kCh; ++c) {
-          float acc = wr[W - 1][c] * xr[c];
-#pragma unroll
-          for (int m = 0; m < W - 1; ++m) acc = fmaf(wr[m][c], win[m][c], acc);
-          y[c] = silu_f32(acc);
-        }
-        Vec8<TX>::store(out + (tb + u) * a.o_s0 + d0, y);
-#pragma unroll
-        for (int m = 0; m < W - 2; ++m)
-#pragma unroll
-          for (int c = 0; c < kCh; ++c) win[m][c] = win[m + 1][c];
-#pragma unroll
-        for (int c = 0; c < kCh; ++c) win[W - 2][c] = xr[c];
-      }
+      const uint32_t r = (uint32_t)(r0 + u < nt ? r0 + u : nt - 1);
+      dst[u].load(reinterpret_cast<const TX*>(reinterpret_cast<const char*>(xt) + r * xs * (uint32_t)sizeof(TX)));
     }
   };
-  load_batch(t0, xa);
-  for (int64_t tb = t0; tb < t1; tb += 2 * kBatch) {
-    if (tb + kBatch < t1) load_batch(tb + kBatch, xb);
-    run_batch(tb, xa);
-    if (tb + kBatch >= t1) break;
-    if (tb + 2 * kBatch < t1) load_batch(tb + 2 * kBatch, xa);
-    run_batch(tb + kBatch, xb);
+  auto run_batch = [&](int r0, const Raw8<TX>* raw) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      float xr[kCh], y[kCh];
+      raw[u].expand(xr);
+#pragma unroll
+      for (int c = 0; c < kCh; ++c) {
+        float acc = wr[W - 1][c] * xr[c];
+#pragma unroll
+        for (int m = 0; m < W - 1; ++m) acc = fmaf(wr[m][c], win[m][c], acc);
+        y[c] = silu_from_scaled(acc);
+      }
+      if (r0 + u < nt)
+        Vec8<TX>::store(reinterpret_cast<TX*>(reinterpret_cast<char*>(ot) + (uint32_t)(r0 + u) * os * (uint32_t)sizeof(TX)), y);
+#pragma unroll
+      for (int m = 0; m < W - 2; ++m)
+#pragma unroll
+        for (int c = 0; c < kCh; ++c) win[m][c] = win[m + 1][c];
+#pragma unroll
+      for (int c = 0; c < kCh; ++c) win[W - 2][c] = xr[c];
+    }
+  };
+  static_assert(kTile % (2 * kBatch) == 0, "whole batch pairs");
+  load_batch(0, xa);
+#pragma unroll
+  for (int r = 0; r < kTile; r += 2 * kBatch) {
+    load_batch(r + kBatch, xb);
+    run_batch(r, xa);
+    if (r + 2 * kBatch < kTile) load_batch(r + 2 * kBatch, xa);
+    run_batch(r + kBatch, xb);
   }
 
   if (tile == 0) {  // new state = last W-1 rows of [old state; x_seq]
@@ -132,6 +172,24 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs
       Vec8<TS>::store(st + r * a.st_s1, row);
     }
   }
+}
+
+// One workgroup per (tile, channel block); blockIdx.x is the linear tile id.
+template <typename TX, typename TW, typename TS, int W>
+__global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs a) {
+  __shared__ int32_t lds[8];
+  const int64_t d0 = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * kCh;
+  const bool active = d0 < a.D;
+  // the taps depend only on the channel block: their loads overlap the lookup
+  float wr[W][kCh];
+  if (active) {
+    load_weights<TW, W>(a, d0, wr);
+    scale_taps(wr, W);
+  }
+  int64_t seq, tile;
+  find_seq_tile<kThreads>(a.cu, a.cu64, a.nseq, a.T, kTile, blockIdx.x, seq, tile, lds);
+  if (seq < 0 || !active) return;
+  conv_tile<TX, TS, W>(a, seq, tile, d0, wr);
 }
 
 template <typename TX, typename TW, typename TS, int W>
@@ -152,14 +210,17 @@ __global__ __launch_bounds__(kThreads) void causal_conv1d_step_kernel(ConvArgs a
   for (int m = 0; m < W - 1; ++m) Vec8<TS>::load(st + m * a.st_s1, xt[m]);
   Vec8<TX>::load(reinterpret_cast<const TX*>(a.x) + b * a.x_s0 + d0, xt[W - 1]);
   float wr[W][kCh];
-  load_weights<TW>(a, d0, W, wr);
+  load_weights<TW, W>(a, d0, wr);
+  scale_taps(wr, W);
   float y[kCh];
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
-    float acc = 0.f;
+    // same order as the prefill kernel (newest tap first), so a decode update
+    // and a one-token prefill give identical bits
+    float acc = wr[W - 1][c] * xt[W - 1][c];
 #pragma unroll
-    for (int m = 0; m < W; ++m) acc = fmaf(wr[m][c], xt[m][c], acc);
-    y[c] = silu_f32(acc);
+    for (int m = 0; m < W - 1; ++m) acc = fmaf(wr[m][c], xt[m][c], acc);
+    y[c] = silu_from_scaled(acc);
   }
   Vec8<TX>::store(out, y);
 #pragma unroll

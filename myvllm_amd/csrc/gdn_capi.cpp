@@ -176,6 +176,8 @@ int check_conv(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, c
     if (!vec_ok(cs, 16)) return GDN_ERR_ALIGN;
   }
   if (T > kMaxGrid || D / 8 > kMaxGrid) return GDN_ERR_RANGE;
+  // the varlen kernel addresses the rows of a 64-token tile with 32-bit byte offsets
+  if (x->stride[0] > (int64_t(1) << 23) || out->stride[0] > (int64_t(1) << 23)) return GDN_ERR_RANGE;
   return GDN_OK;
 }
 

@@ -154,52 +154,59 @@ GDN_DEVICE void seq_range(const void* cu, bool cu64, int64_t n, int64_t T, int64
   e = b;
 }
 
-GDN_DEVICE float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the
+// row broadcasts of the last lane of each row).
+GDN_DEVICE int wave_inclusive_scan_i32(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return x;
+}
 
 // Block-wide lookup of the (sequence, tile) pair owning linear tile id
 // `target`, where sequence n is cut into ceil(len_n / tile_len) tiles laid
 // out sequence after sequence.  Every thread of the (256-thread) block must
 // call it; all receive the same answer, seq = -1 when target is past the end.
-// `lds` must hold at least 6 int64 values.
+// Tile counts are 32-bit (the host bounds T and the grid).  `lds` must hold
+// at least 6 int32 values.
 template <int NT>
 GDN_DEVICE void find_seq_tile(const void* cu, bool cu64, int64_t nseq, int64_t T, int tile_len, int64_t target,
-                              int64_t& seq, int64_t& tile, int64_t* lds) {
+                              int64_t& seq, int64_t& tile, int32_t* lds) {
   static_assert(NT == 256, "find_seq_tile assumes 256 threads");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  __syncthreads();  // a previous call's readers of lds[4], lds[5] are done
   if (tid == 0) { lds[4] = -1; lds[5] = 0; }
   int64_t running = 0;
   for (int64_t base = 0; base < nseq; base += NT) {
     const int64_t n = base + tid;
-    int64_t cnt = 0;
+    int cnt = 0;
     if (n < nseq) {
       int64_t s, e;
       seq_range(cu, cu64, n, T, s, e);
-      cnt = (e - s + tile_len - 1) / tile_len;
+      cnt = (int)((e - s + tile_len - 1) / tile_len);
     }
-    // inclusive scan inside the wave
-    int64_t incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      int64_t y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
+    const int incl = wave_inclusive_scan_i32(cnt);
     __syncthreads();  // lds[0..3] free from the previous round
     if (lane == 63) lds[wave] = incl;
     __syncthreads();
-    int64_t wave_off = 0, total = 0;
+    int wave_off = 0, total = 0;
 #pragma unroll
     for (int w = 0; w < NT / 64; ++w) {
-      int64_t tw = lds[w];
+      const int tw = lds[w];
       if (w < wave) wave_off += tw;
       total += tw;
     }
     const int64_t hi = running + wave_off + incl;
     const int64_t lo = hi - cnt;
     if (cnt > 0 && target >= lo && target < hi) {
-      lds[4] = n;
-      lds[5] = target - lo;
+      lds[4] = (int32_t)n;
+      lds[5] = (int32_t)(target - lo);
     }
     running += total;
     __syncthreads();

@@ -76,3 +76,24 @@ def test_conv_update_equals_one_token_prefill(dev):
     y_b = causal_conv1d_fn(x, case.weight.to(dev), st_b, case.idx.to(dev), cu)
     assert torch.equal(y_a, y_b)
     assert torch.equal(st_a, st_b)
+
+
+def test_conv_strided_weight(dev):
+    """A (D, W) weight view of a (W, D) buffer takes the element-wise tap loads."""
+    case = conv_prefill_case([40, 3], seed=13, D=128, W=4, num_slots=4)
+    st_ref = case.state.clone()
+    y_ref = causal_conv1d_fn_ref(case.x, case.weight, st_ref, case.idx, case.cu)
+    w_t = case.weight.t().contiguous().to(dev).t()
+    assert w_t.stride() == (1, 128)
+    st = case.state.to(dev)
+    y = causal_conv1d_fn(case.x.to(dev), w_t, st, case.idx.to(dev), case.cu.to(dev))
+    assert_out_close(y.cpu(), y_ref)
+    assert torch.equal(st.cpu(), st_ref)
+    st2 = case.state.to(dev)
+    x1 = case.x[:2].to(dev)
+    idx2 = case.idx.to(dev)
+    y2 = causal_conv1d_update(x1, w_t, st2, idx2)
+    st2_ref = case.state.clone()
+    y2_ref = causal_conv1d_update_ref(case.x[:2], case.weight, st2_ref, case.idx)
+    assert_out_close(y2.cpu(), y2_ref)
+    assert torch.equal(st2.cpu(), st2_ref)
