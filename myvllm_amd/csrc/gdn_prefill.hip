@@ -58,7 +58,6 @@ constexpr int KD = 128;    // key head dim
 constexpr int VD = 128;    // value head dim
 constexpr int LDK = 136;   // fp16 row stride of the K/Q tiles
 constexpr int LDV = 144;   // bf16 row stride of the V tile (conflict-free transposed reads)
-constexpr int LDS32 = 32;  // fp32 row stride of a 32x32 diagonal block being solved (rows 16-byte aligned)
 constexpr int LDH = 68;    // fp16 row stride of T_hi/T_lo/P
 constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this many sequences
 constexpr int kSpinLimit = 1 << 22;  // bound on a producer barrier wait (never reached when correct)
@@ -81,36 +80,40 @@ struct PrefillArgs {
   bool idx64, cu64;
 };
 
-// One chunk's on-chip data (80,400 bytes); the kernel holds two.
-struct ChunkSlot {
+// On-chip data.  The state waves work on chunk c while the producers stage
+// chunk c + 1 and solve the diagonal blocks of T' for chunk c + 2:
+//  * per-chunk tiles, double-buffered by chunk parity (44,560 bytes each);
+//  * T' of three consecutive chunks, rotating (17,408 bytes each);
+//  * one V tile: the state waves signal when they have read chunk c's
+//    values, and only then is chunk c + 1's written.
+struct ChunkTiles {
   f16_t k[C * LDK];
-  f16_t q[C * LDK];
-  bf16_t v[C * LDV];  // chunk values, then the staging buffer of the chunk's output
-  union {
-    struct {
-      // T' = (I + A)^-1 diag(beta) as fp16 hi + lo.  Block (0,1) (rows 0..31,
-      // columns 32..63) of T' is zero and never read by the state waves; the
-      // producers keep B_10 there (see prepare_chunk).
-      f16_t hi[C * LDH];
-      f16_t lo[C * LDH];
-    } t;
-    int32_t lens[kMaxRankedSeqs];  // sequence lengths, before the first chunk
-  } u;
-  // P (fp16).  Before P is written, the two 32x32 diagonal blocks of A are
-  // solved here in fp32 (2 x 32 rows of LDS32 floats).
-  f16_t p[C * LDH];
+  f16_t q[C * LDK];  // chunk queries; after the Q S products, the output staging (bf16)
+  f16_t p[C * LDH];  // P (fp16), lower triangle
   alignas(16) float gam[C];
   alignas(16) float eg[C];    // e^gamma
   alignas(16) float edec[C];  // e^(gamma_L - gamma), 0 past the chunk's last token
   alignas(16) float beta[C];
   float gam_last;
 };
-static_assert(2 * 32 * LDS32 * sizeof(float) <= sizeof(f16_t) * C * LDH, "solve scratch must fit the P region");
+
+// T' = (I + A)^-1 diag(beta) as fp16 hi + lo.  Block (0,1) (rows 0..31,
+// columns 32..63) is zero and never read by the state waves; the producers
+// keep B_10 there, and while the diagonal blocks are being solved the two
+// off-diagonal blocks hold the fp32 working copies of the diagonal blocks.
+struct TBuf {
+  f16_t hi[C * LDH];
+  f16_t lo[C * LDH];
+};
 
 struct Smem {
-  ChunkSlot slot[2];
-  int32_t kq_ready;      // arrivals at the producers' first barrier (3 per chunk)
-  int32_t solve_done;    // arrivals at the producers' second barrier (4 per chunk)
+  ChunkTiles tiles[2];
+  TBuf tb[3];
+  bf16_t v[C * LDV];
+  alignas(16) float dvec[2][2][C];  // waves 4, 5: gamma and beta of the chunk they solve
+  int32_t kv_ready;  // chunks whose K tile and decay vectors are staged (wave 6 -> 7)
+  int32_t v_free;    // state-wave arrivals after reading the V tile (4 per chunk)
+  int32_t pro;       // producer arrivals at the prologue barrier
   int32_t seq;
 };
 
@@ -281,13 +284,31 @@ GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
 // so each diagonal block is solved on its own (one wave each) and the
 // off-diagonal block needs only the fp16 hi/lo of T'_00, T'_11 and B_10.
 
-// 16x16 diagonal blocks of a 32x32 strictly lower block A (fp32, stride
-// LDS32) by right-looking forward substitution, in place: lane (b, c) =
-// ((lane / 16) % 2, lane % 16) computes column c of block b; lanes 32..63
-// repeat lanes 0..31 and do not store.
-GDN_DEVICE void invert_diag16(float* A, int lane) {
+// fp32 working copy of a 32x32 diagonal block, kept in the two fp16 arrays
+// of an off-diagonal block of the same T' buffer: row i's columns 0..15 in
+// the hi array, 16..31 in the lo array (64 bytes each, 8-byte aligned).
+struct Scratch {
+  char* hi;  // byte address of the block's row 0 in the hi array
+  char* lo;
+  GDN_DEVICE float* row(int i, int half) const { return reinterpret_cast<float*>((half ? lo : hi) + i * (2 * LDH)); }
+  GDN_DEVICE float& at(int i, int j) const { return row(i, j >> 4)[j & 15]; }
+};
+// diagonal block blk (0 or 1) of tb is worked on in its off-diagonal block (0,1) or (1,0)
+GDN_DEVICE Scratch scratch_of(TBuf& tb, int blk) {
+  const int off = blk == 0 ? 32 : 32 * LDH;  // halves
+  return {reinterpret_cast<char*>(tb.hi + off), reinterpret_cast<char*>(tb.lo + off)};
+}
+GDN_DEVICE f32x4 load4(const float* p) {
+  const f32x2 a = *reinterpret_cast<const f32x2*>(p), b = *reinterpret_cast<const f32x2*>(p + 2);
+  return (f32x4){a[0], a[1], b[0], b[1]};
+}
+
+// 16x16 diagonal blocks of a 32x32 strictly lower block A (fp32) by
+// right-looking forward substitution, in place: lane (b, c) = ((lane / 16) % 2,
+// lane % 16) computes column c of block b; lanes 32..63 repeat lanes 0..31 and
+// do not store.
+GDN_DEVICE void invert_diag16(const Scratch& A, int lane) {
   const int b = (lane >> 4) & 1, c = lane & 15;
-  float* Ab = A + 16 * b * LDS32 + 16 * b;
   float y[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) y[i] = i == c ? 1.f : 0.f;
@@ -295,11 +316,11 @@ GDN_DEVICE void invert_diag16(float* A, int lane) {
   for (int kk = 0; kk < 15; ++kk) {
     const float xk = y[kk];
 #pragma unroll
-    for (int i = kk + 1; i < 16; ++i) y[i] = fmaf(-Ab[i * LDS32 + kk], xk, y[i]);
+    for (int i = kk + 1; i < 16; ++i) y[i] = fmaf(-A.row(16 * b + i, b)[kk], xk, y[i]);
   }
   if (lane < 32) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Ab[i * LDS32 + c] = y[i];
+    for (int i = 0; i < 16; ++i) A.row(16 * b + i, b)[c] = y[i];
   }
 }
 
@@ -313,15 +334,15 @@ GDN_DEVICE void split4(f32x4 x, f16x4& hi, f16x4& lo) {
 
 // 16 -> 32 merge inside a 32x32 block whose diagonal 16-blocks hold their
 // inverses: T_10 = -T_11 A_10 T_00, with 16x16x16 MFMAs on hi/lo splits.
-GDN_DEVICE void merge16(float* A, int lane) {
+GDN_DEVICE void merge16(const Scratch& A, int lane) {
   const int n = lane & 15, g4 = 4 * (lane >> 4);
   f16x4 ah, al, bh, bl;
   // M = A_10 T_00: A operand = rows of A_10, B operand = columns of T_00
-  split4(*reinterpret_cast<const f32x4*>(A + (16 + n) * LDS32 + g4), ah, al);
+  split4(load4(A.row(16 + n, 0) + g4), ah, al);
   {
     f32x4 y;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) y[m] = A[(g4 + m) * LDS32 + n];
+    for (int m = 0; m < 4; ++m) y[m] = A.row(g4 + m, 0)[n];
     split4(y, bh, bl);
   }
   f32x4 M = {0.f, 0.f, 0.f, 0.f};
@@ -329,21 +350,23 @@ GDN_DEVICE void merge16(float* A, int lane) {
   M = mfma16(ah, bl, M);
   M = mfma16(al, bh, M);
   // T_10 = -T_11 M: A operand = rows of T_11, B operand = M (C layout rows == k)
-  split4(*reinterpret_cast<const f32x4*>(A + (16 + n) * LDS32 + 16 + g4), ah, al);
+  split4(load4(A.row(16 + n, 1) + g4), ah, al);
   split4(M, bh, bl);
   f32x4 R = {0.f, 0.f, 0.f, 0.f};
   R = mfma16(ah, bh, R);
   R = mfma16(ah, bl, R);
   R = mfma16(al, bh, R);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) A[(16 + g4 + m) * LDS32 + n] = -R[m];
+  for (int m = 0; m < 4; ++m) A.row(16 + g4 + m, 0)[n] = -R[m];
 }
 
 // Sequence of rank `rank` in longest-first order (ties by index); called by
-// every thread of the block (the lengths are staged in slot 1, unused yet).
+// every thread of the block (the lengths are staged in T' buffer 2, which is
+// first written for chunk 2).
 GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int tid) {
   if (a.nseq > kMaxRankedSeqs) return rank;
-  int32_t* lens = sm.slot[1].u.lens;
+  static_assert(kMaxRankedSeqs * sizeof(int32_t) <= sizeof(TBuf), "lengths fit a T' buffer");
+  int32_t* lens = reinterpret_cast<int32_t*>(sm.tb[2].hi);
   for (int64_t i = tid; i < a.nseq; i += kThreads) {
     int64_t s, e;
     seq_range(a.cu, a.cu64, i, a.T, s, e);
@@ -382,31 +405,6 @@ GDN_DEVICE void producer_wait(int32_t* count, int32_t target) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// A chunk's inputs in flight in registers.  Waves 4, 5 (solvers of the
-// diagonal blocks of T'): r[0..7] = K fragments of their 32 rows (lane (n, g)
-// holds row 32 pw + n, columns 16 ks + 8 g .. +7), r[8..15] = half of V;
-// g and beta (raw bits) of token `lane`.  Waves 6, 7: r[0..7] = half of K,
-// r[8..15] = half of Q, as 16-byte row pieces.
-//
-// Rows past the chunk's last token are loaded from the last token instead
-// (no divergent loads, so nothing waits on them here): they are inert
-// because their g, beta and e^(gamma_L - gamma) are set to zero, which zeroes
-// their rows and columns of T' and their share of the state update, and
-// their output rows are not stored.
-struct ChunkLoad {
-  bf16x8 r[16];
-  float g;
-  ScalarRaw b;
-};
-
-// 16 bytes of row `row` of a chunk (uniform base pointer of the chunk's first
-// token + a 32-bit lane offset; the host guarantees 64 token strides fit).
-GDN_DEVICE bf16x8 load_row_piece(const bf16_t* chunk_base, uint32_t stride, int row, int col, int Lc) {
-  const uint32_t rc = (uint32_t)(row < Lc ? row : Lc - 1);
-  const uint32_t byte_off = (rc * stride + (uint32_t)col) * (uint32_t)sizeof(bf16_t);
-  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(chunk_base) + byte_off);
-}
-
 // Where a (sequence, v-head) reads its chunks from.
 struct ChunkSource {
   const PrefillArgs* a;
@@ -417,48 +415,62 @@ struct ChunkSource {
   int64_t e;         // end token of the sequence
 };
 
-enum LoadPart { kLoadKFrag, kLoadVGB, kLoadKQ };
-
-// One part of the loads of the chunk starting at token c0 (see ChunkLoad).
-GDN_DEVICE void load_part(ChunkLoad& cl, const ChunkSource& src, int64_t c0, LoadPart part, int pw, int lane) {
-  const PrefillArgs& a = *src.a;
+GDN_DEVICE int chunk_rows(const ChunkSource& src, int64_t c0) {
   const int64_t rem = src.e - c0;
-  const int Lc = (int)(rem < C ? rem : C);
-  const int t2 = ((pw & 1) << 6) | lane;  // thread index within the wave pair
-  if (part == kLoadKFrag) {
-    const bf16_t* kb = src.kg + c0 * a.k_s0;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      cl.r[ks] = load_row_piece(kb, (uint32_t)a.k_s0, 32 * pw + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
-  } else if (part == kLoadVGB) {
-    const bf16_t* vb = src.vg + c0 * a.v_s0;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int vec = t2 + 128 * u;
-      cl.r[8 + u] = load_row_piece(vb, (uint32_t)a.v_s0, vec >> 4, 8 * (vec & 15), Lc);
-    }
-    const int64_t t = c0 + (lane < Lc ? lane : Lc - 1);
-    cl.g = a.g[t * a.g_s0 + src.h * a.g_s1];
-    cl.b = load_scalar_raw(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
-  } else {
-    const bf16_t* kb = src.kg + c0 * a.k_s0;
-    const bf16_t* qb = src.qg + c0 * a.q_s0;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int vec = t2 + 128 * u;
-      cl.r[u] = load_row_piece(kb, (uint32_t)a.k_s0, vec >> 4, 8 * (vec & 15), Lc);
-      cl.r[8 + u] = load_row_piece(qb, (uint32_t)a.q_s0, vec >> 4, 8 * (vec & 15), Lc);
-    }
-  }
+  return (int)(rem < C ? rem : C);
 }
 
-GDN_DEVICE void load_chunk(ChunkLoad& cl, const ChunkSource& src, int64_t c0, int pw, int lane) {
-  if (pw < 2) {
-    load_part(cl, src, c0, kLoadKFrag, pw, lane);
-    load_part(cl, src, c0, kLoadVGB, pw, lane);
-  } else {
-    load_part(cl, src, c0, kLoadKQ, pw, lane);
-  }
+// Rows past the chunk's last token are loaded from the last token instead
+// (no divergent loads, so nothing waits on them early): they are inert
+// because their g, beta and e^(gamma_L - gamma) are set to zero, which zeroes
+// their rows and columns of T' and their share of the state update, and
+// their output rows are not stored.
+//
+// 16 bytes of row `row` of a chunk (uniform base pointer of the chunk's first
+// token + a 32-bit lane offset; the host guarantees 64 token strides fit).
+GDN_DEVICE bf16x8 load_row_piece(const bf16_t* chunk_base, uint32_t stride, int row, int col, int Lc) {
+  const uint32_t rc = (uint32_t)(row < Lc ? row : Lc - 1);
+  const uint32_t byte_off = (rc * stride + (uint32_t)col) * (uint32_t)sizeof(bf16_t);
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(chunk_base) + byte_off);
+}
+
+// A whole 64 x 128 chunk tile in one wave's registers: vector u of lane l is
+// row l / 16 + 4u, columns 8 (l % 16) .. +7.
+struct TileLoad {
+  bf16x8 r[16];
+};
+GDN_DEVICE void load_tile(TileLoad& tl, const bf16_t* head_base, int64_t stride, int64_t c0, int Lc, int lane) {
+  const bf16_t* b = head_base + c0 * stride;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) tl.r[u] = load_row_piece(b, (uint32_t)stride, (lane >> 4) + 4 * u, 8 * (lane & 15), Lc);
+}
+
+// g and beta (raw bits) of token `lane` of a chunk.
+struct DecayLoad {
+  float g;
+  ScalarRaw b;
+};
+GDN_DEVICE void load_decay(DecayLoad& dl, const ChunkSource& src, int64_t c0, int Lc, int lane) {
+  const PrefillArgs& a = *src.a;
+  const int64_t t = c0 + (lane < Lc ? lane : Lc - 1);
+  dl.g = a.g[t * a.g_s0 + src.h * a.g_s1];
+  dl.b = load_scalar_raw(a.beta, t * a.b_s0 + src.h * a.b_s1, a.b_dtype);
+}
+
+// K fragments of a diagonal block's 32 rows (lane (n, g) holds row 32 blk + n,
+// columns 16 ks + 8 g .. +7) and the chunk's decays.
+struct DiagLoad {
+  bf16x8 kf[8];
+  DecayLoad d;
+};
+GDN_DEVICE void load_diag(DiagLoad& dl, const ChunkSource& src, int64_t c0, int blk, int lane) {
+  const PrefillArgs& a = *src.a;
+  const int Lc = chunk_rows(src, c0);
+  const bf16_t* kb = src.kg + c0 * a.k_s0;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+    dl.kf[ks] = load_row_piece(kb, (uint32_t)a.k_s0, 32 * blk + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
+  load_decay(dl.d, src, c0, Lc, lane);
 }
 
 // bf16 -> fp16 of 8 values (exact for |x| in the fp16 normal range): the
@@ -475,6 +487,14 @@ GDN_DEVICE f16x8 bf16x8_to_f16x8(bf16x8 x) {
   return __builtin_bit_cast(f16x8, o);
 }
 
+// gamma = in-chunk cumsum of g (one token per lane) and the per-token decay
+// vectors; g and beta of tokens past the chunk end are taken as zero.
+GDN_DEVICE float chunk_gamma(const DecayLoad& dl, int L, int lane, float& gl) {
+  const float gm = wave_inclusive_scan(lane < L ? dl.g : 0.f);
+  gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gm), 63));  // gamma at token L-1
+  return gm;
+}
+
 // Gram tile (mt, nt) of rows of M1 against rows of M2 (K = 128): C layout,
 // lane holds column 32nt + n, rows 32mt + 8i + 4g + r.
 GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, int lane) {
@@ -485,42 +505,42 @@ GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, in
   return G;
 }
 
-// Diagonal block `blk` of T': A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
-// from the kk^T tile (K fragments in registers), solved in fp32 in the wave's scratch block (16x16
-// substitution + one MFMA merge), then T'_bb = T_bb diag(beta) written as
-// fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's LDS
-// accesses complete in program order.
 // kk^T of a diagonal block's rows from the register fragments (bf16 holds k exactly)
-GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[16]) {
+GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[8]) {
   f32x16 G = zero16();
 #pragma unroll
   for (int ks = 0; ks < KD / 16; ++ks) G = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], kf[ks], G, 0, 0, 0);
   return G;
 }
 
-GDN_DEVICE void solve_diag_block(ChunkSlot& cs, int blk, const f32x16& G, int lane) {
+// Diagonal block `blk` of T': A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
+// from its kk^T tile, solved in fp32 in the off-diagonal block of the same
+// T' buffer (16x16 substitution + one MFMA merge), then T'_bb = T_bb diag(beta)
+// written as fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's
+// LDS accesses complete in program order.  gam and beta: the chunk's vectors.
+GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, const f32x16& G, int blk, int lane) {
   const int n = lane & 31, gq = lane >> 5, o = 32 * blk;
-  float* A = reinterpret_cast<float*>(cs.p) + blk * 32 * LDS32;
-  const float gj = cs.gam[o + n];
+  const Scratch A = scratch_of(tb, blk);
+  const float gj = gam[o + n];
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
-    const f32x4 gi = rows4(cs.gam, o, i4, lane);
-    const f32x4 bi = rows4(cs.beta, o, i4, lane);
+    const f32x4 gi = rows4(gam, o, i4, lane);
+    const f32x4 bi = rows4(beta, o, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = 8 * i4 + 4 * gq + rr;
-      A[i * LDS32 + n] = i > n ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+      A.at(i, n) = i > n ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
     }
   }
   invert_diag16(A, lane);
   merge16(A, lane);
   // T'_bb = T_bb diag(beta): lane -> row lane / 2, 16 columns
-  const int i = lane >> 1, j0 = 16 * (lane & 1);
+  const int i = lane >> 1, half = lane & 1, j0 = 16 * half;
   float tv[16];
 #pragma unroll
   for (int m = 0; m < 16; m += 4) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(A + i * LDS32 + j0 + m);
-    const f32x4 bb = *reinterpret_cast<const f32x4*>(cs.beta + o + j0 + m);
+    const f32x4 x = load4(A.row(i, half) + m);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(beta + o + j0 + m);
 #pragma unroll
     for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
   }
@@ -529,39 +549,39 @@ GDN_DEVICE void solve_diag_block(ChunkSlot& cs, int blk, const f32x16& G, int la
 #pragma unroll
   for (int m = 0; m < 16; m += 4) {
     const int off = (o + i) * LDH + o + j0 + m;
-    *reinterpret_cast<f16x4*>(cs.u.t.hi + off) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
-    *reinterpret_cast<f16x4*>(cs.u.t.lo + off) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
+    *reinterpret_cast<f16x4*>(tb.hi + off) = (f16x4){th[m], th[m + 1], th[m + 2], th[m + 3]};
+    *reinterpret_cast<f16x4*>(tb.lo + off) = (f16x4){tl[m], tl[m + 1], tl[m + 2], tl[m + 3]};
   }
 }
 
 // B_10 = k_i.k_j e^(g_i - g_j) for tokens i in 32..63, j in 0..31 (always
 // i > j), as fp16 hi/lo in block (0,1) of the T' arrays: B_10[i][j] at row i,
 // column 32 + j.  |B_10| <= 1, so the split needs no scaling.
-GDN_DEVICE void b10_block(ChunkSlot& cs, int lane) {
+GDN_DEVICE void b10_block(const ChunkTiles& ct, TBuf& tb, int lane) {
   const int n = lane & 31, gq = lane >> 5;
-  const f32x16 G = gram_tile(cs.k, cs.k, 1, 0, lane);
-  const float gj = cs.gam[n];
+  const f32x16 G = gram_tile(ct.k, ct.k, 1, 0, lane);
+  const float gj = ct.gam[n];
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
-    const f32x4 gi = rows4(cs.gam, 32, i4, lane);
+    const f32x4 gi = rows4(ct.gam, 32, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; rr += 2) {
       const int i = 8 * i4 + 4 * gq + rr;
       f16_t h0, h1, l0, l1;
       split_pair(G[4 * i4 + rr] * __expf(gi[rr] - gj), G[4 * i4 + rr + 1] * __expf(gi[rr + 1] - gj), h0, h1, l0, l1);
-      cs.u.t.hi[i * LDH + 32 + n] = h0;
-      cs.u.t.hi[(i + 1) * LDH + 32 + n] = h1;
-      cs.u.t.lo[i * LDH + 32 + n] = l0;
-      cs.u.t.lo[(i + 1) * LDH + 32 + n] = l1;
+      tb.hi[i * LDH + 32 + n] = h0;
+      tb.hi[(i + 1) * LDH + 32 + n] = h1;
+      tb.lo[i * LDH + 32 + n] = l0;
+      tb.lo[(i + 1) * LDH + 32 + n] = l1;
     }
   }
 }
 
 // T'_10 = -T'_11 B_10 T'_00 from the fp16 hi/lo blocks (lo x lo dropped).  One wave.
-GDN_DEVICE void merge_offdiag(ChunkSlot& cs, int lane) {
+GDN_DEVICE void merge_offdiag(TBuf& tb, int lane) {
   const int n = lane & 31, gq = lane >> 5;
-  const f16_t* th = cs.u.t.hi;
-  const f16_t* tl = cs.u.t.lo;
+  const f16_t* th = tb.hi;
+  const f16_t* tl = tb.lo;
   // M = B_10 T'_00: A operand = rows of B_10, B operand = columns of T'_00
   f32x16 M = zero16();
 #pragma unroll
@@ -588,23 +608,23 @@ GDN_DEVICE void merge_offdiag(ChunkSlot& cs, int lane) {
     const int i = 32 + 8 * (j >> 2) + 4 * gq + (j & 3);
     f16_t h0, h1, l0, l1;
     split_pair(-R[j], -R[j + 1], h0, h1, l0, l1);
-    cs.u.t.hi[i * LDH + n] = h0;
-    cs.u.t.hi[(i + 1) * LDH + n] = h1;
-    cs.u.t.lo[i * LDH + n] = l0;
-    cs.u.t.lo[(i + 1) * LDH + n] = l1;
+    tb.hi[i * LDH + n] = h0;
+    tb.hi[(i + 1) * LDH + n] = h1;
+    tb.lo[i * LDH + n] = l0;
+    tb.lo[(i + 1) * LDH + n] = l1;
   }
 }
 
 // (Q K^T) tile (mt, nt) -> P = lower(q_i.k_j e^(g_i - g_j)) as fp16, C layout
 // (element 4 i4 + rr of the tile at row 32mt + 8 i4 + 4g + rr).
-GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkSlot& cs, int mt, int nt, int h, int lane) {
+GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkTiles& ct, int mt, int nt, int h, int lane) {
   const int n = lane & 31, gq = lane >> 5;
   const int j = 32 * nt + n;
-  const float gj = cs.gam[j];
+  const float gj = ct.gam[j];
   f16x8 out;
 #pragma unroll
   for (int i4 = 2 * h; i4 < 2 * h + 2; ++i4) {
-    const f32x4 gi = rows4(cs.gam, 32 * mt, i4, lane);
+    const f32x4 gi = rows4(ct.gam, 32 * mt, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
@@ -613,101 +633,49 @@ GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkSlot& cs, int mt, int nt, i
   }
   return out;
 }
-struct PTile {
-  f16x8 h[2];
-};
-GDN_DEVICE PTile qk_tile(const ChunkSlot& cs, int mt, int nt, int lane) {
-  const f32x16 G = gram_tile(cs.q, cs.k, mt, nt, lane);
-  PTile t;
-  t.h[0] = qk_half(G, cs, mt, nt, 0, lane);
-  t.h[1] = qk_half(G, cs, mt, nt, 1, lane);
-  return t;
-}
-GDN_DEVICE void store_p(ChunkSlot& cs, const PTile& t, int mt, int nt, int lane) {
+GDN_DEVICE void p_tile(ChunkTiles& ct, int mt, int nt, int lane) {
+  const f32x16 G = gram_tile(ct.q, ct.k, mt, nt, lane);
+  const f16x8 h0 = qk_half(G, ct, mt, nt, 0, lane), h1 = qk_half(G, ct, mt, nt, 1, lane);
   const int n = lane & 31, gq = lane >> 5;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int i = 32 * mt + 8 * (e >> 2) + 4 * gq + (e & 3);
-    cs.p[i * LDH + 32 * nt + n] = t.h[e >> 3][e & 7];
+    ct.p[i * LDH + 32 * nt + n] = e < 8 ? h0[e] : h1[e - 8];
   }
 }
 
-// Everything of a chunk that does not depend on the state, written to slot cs.
-//  * waves 4, 5: stage V and the decay vectors (identical values from both),
-//    then solve their diagonal block of T' from K fragments in registers --
-//    without waiting for anyone;
-//  * waves 6, 7: stage K and Q (fp16), wait for each other and for wave 4's
-//    decay vectors, then form B_10 and the P tiles;
-//  * after a barrier of all four: wave 4 forms T'_10, waves 6, 7 store P.
-GDN_DEVICE void prepare_chunk(ChunkSlot& cs, ChunkLoad& cl, int L, const ChunkSource& src, int64_t next_c0,
-                              bool has_next, Smem& sm, int32_t& t_kq, int32_t& t_solve, int pw, int lane) {
-  asm volatile("" : "+v"(lane));  // as in consume_chunk: no hoisted lane masks
-  const int t2 = ((pw & 1) << 6) | lane;
-  PTile pa, pb;
-  if (pw < 2) {
+// Stage a tile held in registers into LDS (fp16 for K/Q, bf16 as is for V).
+GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int vec = t2 + 128 * u;
-      *reinterpret_cast<bf16x8*>(cs.v + (vec >> 4) * LDV + 8 * (vec & 15)) = cl.r[8 + u];
-    }
-    // gamma = in-chunk cumsum of g, one token per lane
-    const float gm = wave_inclusive_scan(lane < L ? cl.g : 0.f);
-    // padded g is 0, so lane 63 holds gamma at token L-1
-    const float gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gm), 63));
-    cs.gam[lane] = gm;
-    cs.eg[lane] = __expf(gm);
-    cs.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
-    cs.beta[lane] = lane < L ? scalar_raw_f32(cl.b, src.a->b_dtype) : 0.f;
-    if (lane == 0) cs.gam_last = gl;
-    if (pw == 0) producer_arrive(&sm.kq_ready, lane);
-    // the next chunk's loads go out as soon as their registers are free
-    if (has_next) load_part(cl, src, next_c0, kLoadVGB, pw, lane);
-    const f32x16 G = gram_regs(cl.r);
-    if (has_next) load_part(cl, src, next_c0, kLoadKFrag, pw, lane);
-    solve_diag_block(cs, pw, G, lane);
-  } else {
+  for (int u = 0; u < 16; ++u)
+    *reinterpret_cast<f16x8*>(dst + ((lane >> 4) + 4 * u) * LDK + 8 * (lane & 15)) = bf16x8_to_f16x8(tl.r[u]);
+}
+GDN_DEVICE void stage_v(bf16_t* dst, const TileLoad& tl, int lane) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int vec = t2 + 128 * u;
-      const int off = (vec >> 4) * LDK + 8 * (vec & 15);
-      *reinterpret_cast<f16x8*>(cs.k + off) = bf16x8_to_f16x8(cl.r[u]);
-      *reinterpret_cast<f16x8*>(cs.q + off) = bf16x8_to_f16x8(cl.r[8 + u]);
-    }
-    if (has_next) load_part(cl, src, next_c0, kLoadKQ, pw, lane);
-    producer_arrive(&sm.kq_ready, lane);
-    t_kq += 3;
-    producer_wait(&sm.kq_ready, t_kq);
-    if (pw == 2) {
-      b10_block(cs, lane);
-      pa = qk_tile(cs, 1, 0, lane);
-    } else {
-      pa = qk_tile(cs, 0, 0, lane);
-      pb = qk_tile(cs, 1, 1, lane);
-    }
-  }
-  producer_arrive(&sm.solve_done, lane);
-  t_solve += 4;
-  producer_wait(&sm.solve_done, t_solve);
+  for (int u = 0; u < 16; ++u) *reinterpret_cast<bf16x8*>(dst + ((lane >> 4) + 4 * u) * LDV + 8 * (lane & 15)) = tl.r[u];
+}
 
-  if (pw == 0) {
-    merge_offdiag(cs, lane);
-  } else if (pw == 2) {
-    store_p(cs, pa, 1, 0, lane);
-  } else if (pw == 3) {
-    store_p(cs, pa, 0, 0, lane);
-    store_p(cs, pb, 1, 1, lane);
-  }
+// Decay vectors of a chunk for the state waves and the producers' epilogues.
+GDN_DEVICE void stage_decay(ChunkTiles& ct, const DecayLoad& dl, int L, int b_dtype, int lane) {
+  float gl;
+  const float gm = chunk_gamma(dl, L, lane, gl);
+  ct.gam[lane] = gm;
+  ct.eg[lane] = __expf(gm);
+  ct.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
+  ct.beta[lane] = lane < L ? scalar_raw_f32(dl.b, b_dtype) : 0.f;
+  if (lane == 0) ct.gam_last = gl;
 }
 
 // ---- state role (waves 0..3) -----------------------------------------------------
 
 // The state products of one chunk on this wave's 32 value columns; writes the
-// chunk's output rows for those columns.  The state is held in units of
+// chunk's output rows for those columns (staged through its own columns of
+// the V tile, after which it signals v_free).  The state is held in units of
 // 2^su (true state = S * 2^su, su wave-uniform): the update rescales S by
 // one factor per chunk and re-bases su on the exponent of V', so no other
 // pass over S is needed for the fp16 splits.
-GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const PrefillArgs& a, int64_t c0, int L,
-                              int h, int wave, int lane) {
+GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, int32_t* v_free, f32x16 (&S)[4],
+                              int& su, const PrefillArgs& a, int64_t c0, int L, int h, int wave, int lane) {
   // Lane-dependent addresses are cheap to recompute; keeping them out of
   // loop-invariant code motion keeps them out of registers across chunks.
   asm volatile("" : "+v"(lane));
@@ -721,10 +689,10 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
   for (int ks = 0; ks < 8; ++ks) {
     f16x8 shi, slo;
     split8(S[ks >> 1], ks & 1, ss, shi, slo);
-    const f16x8 ak0 = frag_rows(cs.k, LDK, 0, 16 * ks, lane);
-    const f16x8 ak1 = frag_rows(cs.k, LDK, 32, 16 * ks, lane);
-    const f16x8 aq0 = frag_rows(cs.q, LDK, 0, 16 * ks, lane);
-    const f16x8 aq1 = frag_rows(cs.q, LDK, 32, 16 * ks, lane);
+    const f16x8 ak0 = frag_rows(ct.k, LDK, 0, 16 * ks, lane);
+    const f16x8 ak1 = frag_rows(ct.k, LDK, 32, 16 * ks, lane);
+    const f16x8 aq0 = frag_rows(ct.q, LDK, 0, 16 * ks, lane);
+    const f16x8 aq1 = frag_rows(ct.q, LDK, 32, 16 * ks, lane);
     X[0] = mfma32(ak0, shi, X[0]);
     X[1] = mfma32(ak1, shi, X[1]);
     QS[0] = mfma32(aq0, shi, QS[0]);
@@ -739,9 +707,9 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f32x4 egv = rows4(cs.eg, 32 * mt, i, lane);
+      const f32x4 egv = rows4(ct.eg, 32 * mt, i, lane);
       const int j = lane & 15, qd = lane >> 4;
-      const bf16_t* p = cs.v + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
+      const bf16_t* p = vt + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
       const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu), X[mt][4 * i + rr], (float)vv[rr]);
@@ -758,10 +726,10 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
     f16x8 rhi, rlo;
     split8(R[ks >> 1], ks & 1, rs, rhi, rlo);
     if (ks < 2) {
-      const f16x8 ah0 = frag_rows(cs.u.t.hi, LDH, 0, 16 * ks, lane);
-      const f16x8 al0 = frag_rows(cs.u.t.lo, LDH, 0, 16 * ks, lane);
-      const f16x8 ah1 = frag_rows(cs.u.t.hi, LDH, 32, 16 * ks, lane);
-      const f16x8 al1 = frag_rows(cs.u.t.lo, LDH, 32, 16 * ks, lane);
+      const f16x8 ah0 = frag_rows(tb.hi, LDH, 0, 16 * ks, lane);
+      const f16x8 al0 = frag_rows(tb.lo, LDH, 0, 16 * ks, lane);
+      const f16x8 ah1 = frag_rows(tb.hi, LDH, 32, 16 * ks, lane);
+      const f16x8 al1 = frag_rows(tb.lo, LDH, 32, 16 * ks, lane);
       VN[0] = mfma32(ah0, rhi, VN[0]);
       VN[1] = mfma32(ah1, rhi, VN[1]);
       VN[0] = mfma32(ah0, rlo, VN[0]);
@@ -769,8 +737,8 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
       VN[0] = mfma32(al0, rhi, VN[0]);
       VN[1] = mfma32(al1, rhi, VN[1]);
     } else {
-      const f16x8 ah1 = frag_rows(cs.u.t.hi, LDH, 32, 16 * ks, lane);
-      const f16x8 al1 = frag_rows(cs.u.t.lo, LDH, 32, 16 * ks, lane);
+      const f16x8 ah1 = frag_rows(tb.hi, LDH, 32, 16 * ks, lane);
+      const f16x8 al1 = frag_rows(tb.lo, LDH, 32, 16 * ks, lane);
       VN[1] = mfma32(ah1, rhi, VN[1]);
       VN[1] = mfma32(ah1, rlo, VN[1]);
       VN[1] = mfma32(al1, rhi, VN[1]);
@@ -782,7 +750,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f32x4 egv = rows4(cs.eg, 32 * mt, i, lane);
+      const f32x4 egv = rows4(ct.eg, 32 * mt, i, lane);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) QS[mt][4 * i + rr] *= egv[rr] * qsu;
     }
@@ -793,7 +761,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
 #pragma unroll
     for (int m = 0; m < 8; ++m) vb[m] = (f16_t)VN[ks >> 1][8 * (ks & 1) + m];
 #pragma unroll
-    for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(cs.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
+    for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(ct.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
   }
   // stage this wave's output columns (bf16) in the V tile, then store 16-byte row pieces
   {
@@ -803,7 +771,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
 #pragma unroll
       for (int jj = 0; jj < 16; ++jj) {
         const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
-        cs.v[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
+        vt[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
       }
     bf16_t* ob = a.out + c0 * a.o_s0 + h * a.o_s1 + 32 * wave;
 #pragma unroll
@@ -811,9 +779,11 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
       const int row = 16 * u + (lane >> 2), cgp = lane & 3;
       if (row < L)
         *reinterpret_cast<bf16x8*>(reinterpret_cast<char*>(ob) + ((uint32_t)row * (uint32_t)a.o_s0 + 8u * cgp) * 2u) =
-            *reinterpret_cast<const bf16x8*>(cs.v + row * LDV + 32 * wave + 8 * cgp);
+            *reinterpret_cast<const bf16x8*>(vt + row * LDV + 32 * wave + 8 * cgp);
     }
   }
+  // this wave is done with the V tile (its values, then its output staging)
+  producer_arrive(v_free, lane);
   // S_true' = e^gamma_L S_true + K^T Vd, Vd = diag(e^(gamma_L - gamma)) V' = diag(edec) VN 2^er.
   // The split operand is Vd 2^-ed with ed = er + evn (max |VN| 2^-evn in [2^9, 2^10),
   // edec <= 1), and the new state is held in units of 2^ed:
@@ -821,7 +791,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
   // ed >= ex - 64 keeps S' far inside the fp32 range; evn >= -100 keeps 2^(er - ed) finite.
   const int ed = max(er + max(wave_scale_exp(VN, 2), -100), ex - 64);
   const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
-  const float edl = __expf(cs.gam_last);
+  const float edl = __expf(ct.gam_last);
   const int dsu = su - ed;
   if (dsu >= -100 && dsu <= 100) {
     const float sdec = __builtin_amdgcn_ldexpf(edl, dsu);
@@ -840,7 +810,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
     float fd[8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const f32x4 dv = rows4(cs.edec, 32 * (ks >> 1), 2 * (ks & 1) + i, lane);
+      const f32x4 dv = rows4(ct.edec, 32 * (ks >> 1), 2 * (ks & 1) + i, lane);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) fd[4 * i + rr] = dv[rr] * fdu;
     }
@@ -848,7 +818,7 @@ GDN_DEVICE void consume_chunk(ChunkSlot& cs, f32x16 (&S)[4], int& su, const Pref
     split8f(VN[ks >> 1], ks & 1, fd, dhi, dlo);
     f16x8 akt[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(cs.k, LDK, 32 * mt, 16 * ks, lane);
+    for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(ct.k, LDK, 32 * mt, 16 * ks, lane);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dhi, S[mt]);
 #pragma unroll
@@ -870,9 +840,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
   if (work >= a.nseq * a.Hv) return;
   if (tid == 0) {
-    sm.kq_ready = 0;
-    sm.solve_done = 0;
+    sm.kv_ready = 0;
+    sm.v_free = 0;
+    sm.pro = 0;
   }
+  __syncthreads();  // the counters are zero before any wave can arrive
   const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
   const int h = (int)(work % a.Hv);
   const int kh = h / a.r;
@@ -906,30 +878,117 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
-      consume_chunk(sm.slot[c & 1], S, su, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
-      __syncthreads();  // slot (c & 1) is free again, slot ((c + 1) & 1) is prepared
+      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], sm.v, &sm.v_free, S, su, a, s + (int64_t)c * C, chunk_len(c), h,
+                    wave, lane);
+      __syncthreads();  // chunk c + 1 is prepared
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = __builtin_amdgcn_ldexpf(S[mt][j], su);
-  } else {
-    // ---- producer waves: chunk c + 1 while the state waves work on chunk c
-    const int pw = wave - 4;
-    const bf16_t* qg = a.q + kh * a.q_s1;
-    const bf16_t* kg = a.k + kh * a.k_s1;
-    const bf16_t* vg = a.v + h * a.v_s1;
-    int32_t t_kq = 0, t_solve = 0;
-    const ChunkSource src = {&a, kg, qg, vg, h, e};
-    ChunkLoad cl;
-    load_chunk(cl, src, s, pw, lane);
-    prepare_chunk(sm.slot[0], cl, chunk_len(0), src, s + C, nc > 1, sm, t_kq, t_solve, pw, lane);
+    return;
+  }
+
+  // ---- producer waves.  While the state waves work on chunk c:
+  //  waves 4 / 5: diagonal block 0 / 1 of T' for chunk c + 2;
+  //  wave 6: K tile and decay vectors of chunk c + 1, then B_10 and T'_10 of
+  //          chunk c + 1 (its diagonal blocks were solved one iteration earlier);
+  //  wave 7: Q tile and P tiles of chunk c + 1, then its V tile once the
+  //          state waves have released the V tile of chunk c.
+  // Next-chunk loads go out right after the registers have been staged.
+  // A prologue fills the pipeline: diagonal blocks of chunks 0 and 1 and
+  // everything else of chunk 0.
+  const int pw = wave - 4;
+  const ChunkSource src = {&a, a.k + kh * a.k_s1, a.q + kh * a.q_s1, a.v + h * a.v_s1, h, e};
+  auto c0_of = [&](int c) { return s + (int64_t)c * C; };
+  if (pw < 2) {
+    float* dgam = sm.dvec[pw][0];
+    float* dbeta = sm.dvec[pw][1];
+    DiagLoad dl;
+    // solve this wave's diagonal block of chunk c (its loads are in dl) into
+    // T' buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
+    auto solve = [&](int c) {
+      float gl;
+      const int L = chunk_len(c);
+      dgam[lane] = chunk_gamma(dl.d, L, lane, gl);
+      dbeta[lane] = lane < L ? scalar_raw_f32(dl.d.b, a.b_dtype) : 0.f;
+      const f32x16 G = gram_regs(dl.kf);
+      if (c + 1 < nc) load_diag(dl, src, c0_of(c + 1), pw, lane);
+      solve_diag_block(sm.tb[c % 3], dgam, dbeta, G, pw, lane);
+    };
+    load_diag(dl, src, c0_of(0), pw, lane);
+    solve(0);
+    producer_arrive(&sm.pro, lane);
+    producer_wait(&sm.pro, 4);
+    if (nc > 1) solve(1);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+      if (c + 2 < nc) solve(c + 2);
+      __syncthreads();
+    }
+  } else if (pw == 2) {
+    TileLoad kl;
+    DecayLoad dl;
+    auto load = [&](int c) {
+      const int Lc = chunk_rows(src, c0_of(c));
+      load_tile(kl, src.kg, a.k_s0, c0_of(c), Lc, lane);
+      load_decay(dl, src, c0_of(c), Lc, lane);
+    };
+    // K tile and decay vectors of chunk c into tile set c & 1, then release wave 7
+    auto stage = [&](int c) {
+      ChunkTiles& ct = sm.tiles[c & 1];
+      stage_f16(ct.k, kl, lane);
+      stage_decay(ct, dl, chunk_len(c), a.b_dtype, lane);
+      producer_arrive(&sm.kv_ready, lane);
+    };
+    auto offdiag = [&](int c) {
+      b10_block(sm.tiles[c & 1], sm.tb[c % 3], lane);
+      merge_offdiag(sm.tb[c % 3], lane);
+    };
+    load(0);
+    stage(0);
+    producer_arrive(&sm.pro, lane);
+    producer_wait(&sm.pro, 4);
+    offdiag(0);
+    if (nc > 1) load(1);
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
       if (c + 1 < nc) {
-        prepare_chunk(sm.slot[(c + 1) & 1], cl, chunk_len(c + 1), src, s + (int64_t)(c + 2) * C, c + 2 < nc, sm, t_kq,
-                      t_solve, pw, lane);
+        stage(c + 1);
+        if (c + 2 < nc) load(c + 2);
+        offdiag(c + 1);
+      }
+      __syncthreads();
+    }
+  } else {
+    TileLoad ql, vl;
+    auto qload = [&](int c) { load_tile(ql, src.qg, a.q_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
+    auto vload = [&](int c) { load_tile(vl, src.vg, a.v_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
+    // Q tile and the three P tiles of chunk c
+    auto qp = [&](int c) {
+      ChunkTiles& ct = sm.tiles[c & 1];
+      stage_f16(ct.q, ql, lane);
+      if (c + 1 < nc) qload(c + 1);
+      producer_wait(&sm.kv_ready, c + 1);
+      p_tile(ct, 0, 0, lane);
+      p_tile(ct, 1, 0, lane);
+      p_tile(ct, 1, 1, lane);
+    };
+    qload(0);
+    vload(0);
+    qp(0);
+    stage_v(sm.v, vl, lane);
+    if (nc > 1) vload(1);
+    producer_arrive(&sm.pro, lane);
+    producer_wait(&sm.pro, 4);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+      if (c + 1 < nc) {
+        qp(c + 1);
+        producer_wait(&sm.v_free, 4 * (c + 1));  // the state waves are done with chunk c's V tile
+        stage_v(sm.v, vl, lane);
+        if (c + 2 < nc) vload(c + 2);
       }
       __syncthreads();
     }
