@@ -42,10 +42,10 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_052_598_584,
-    "gdn_recurrent_step_kernel": 1_083_318_318,
-    "causal_conv1d_varlen_kernel": 680_914_206,
-    "causal_conv1d_step_kernel": 59_431_379,
+    "gdn_chunk_prefill_kernel": 1_075_139_713,
+    "gdn_recurrent_step_kernel": 1_083_193_349,
+    "causal_conv1d_varlen_kernel": 665_911_711,
+    "causal_conv1d_step_kernel": 59_314_135,
 }
 
 
