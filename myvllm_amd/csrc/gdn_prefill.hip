@@ -225,25 +225,25 @@ GDN_DEVICE void split_pair(float x0, float x1, f16_t& h0, f16_t& h1, f16_t& l0, 
   l1 = l[1];
 }
 
-// Scaled fp16 hi/lo pairs with the mixed-precision FMAs: hi = fp16(x s) and
-// lo = fp16(x s - hi), each rounded once from the exact product, so lo is
-// referenced to exactly the stored hi bits.  A scale per element lets a
-// per-row factor ride along (C-layout neighbours are adjacent rows).
+// Scaled fp16 hi/lo pairs: hi = fp16(x s) and lo = fp16(x s - hi) (s a
+// power of two times a per-element factor, so x s - hi is exact in fp32 and
+// each half is rounded once).  hi's bits are pinned through an empty asm, so
+// lo is referenced to exactly the stored hi bits whichever conversion
+// instructions the compiler picks for the two uses.  (Plain code rather than
+// hand-written v_fma_mix* instructions: the compiler pads an MFMA's operand
+// reads after VALU writes only for instructions it generated itself.)  A
+// scale per element lets a per-row factor ride along (C-layout neighbours
+// are adjacent rows).
 GDN_DEVICE uint32_t mix_hi_pair(float x0, float s0, float x1, float s1) {
-  uint32_t h;
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]\n\t"
-      "v_fma_mixhi_f16 %0, %3, %4, 0 op_sel_hi:[0,0,0]"
-      : "=&v"(h)
-      : "v"(x0), "v"(s0), "v"(x1), "v"(s1));
-  return h;
+  const f16x2 h = {(f16_t)(x0 * s0), (f16_t)(x1 * s1)};
+  uint32_t hb = __builtin_bit_cast(uint32_t, h);
+  asm volatile("" : "+v"(hb));
+  return hb;
 }
-GDN_DEVICE uint32_t mix_lo_pair(float x0, float s0, float x1, float s1, uint32_t h) {
-  uint32_t l;
-  asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel_hi:[0,0,1]\n\t"
-      "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-      : "=&v"(l)
-      : "v"(x0), "v"(s0), "v"(x1), "v"(s1), "v"(h));
-  return l;
+GDN_DEVICE uint32_t mix_lo_pair(float x0, float s0, float x1, float s1, uint32_t hb) {
+  const f16x2 h = __builtin_bit_cast(f16x2, hb);
+  const f16x2 l = {(f16_t)__builtin_fmaf(x0, s0, -(float)h[0]), (f16_t)__builtin_fmaf(x1, s1, -(float)h[1])};
+  return __builtin_bit_cast(uint32_t, l);
 }
 
 // split of registers 8h..8h+7 of a C tile, times sc
