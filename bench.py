@@ -7,8 +7,10 @@ lengths uniform in [512, 4096] -> 35,846 tokens, Hk 16 / Hv 32, d 128,
 chunk 64, bf16 q/k/v, fp32 g/beta and state).  The same line carries the
 recurrent decode step (batch 256, fp32 state gathered from a 1024-slot
 cache, HBM GB/s), the varlen causal conv1d (8 sequences, 19,762 tokens,
-8192 channels, width 4) and the conv decode update (batch 256), each with
-its roofline and the CPU oracle timed on this host.
+8192 channels, width 4), the conv decode update (batch 256) and the fused
+decode step (conv update + L2 norm + gating + recurrent step, batch 256,
+with the same step as separate ops timed beside it), each with its
+roofline and, where it applies, the CPU oracle timed on this host.
 
 A step is one call of the op on inputs already resident in HBM.  Timing:
 W untimed warm-up steps, then K steps bracketed by device synchronisation;
@@ -236,6 +238,50 @@ def bench_conv_update(dev, steps, warmup, cpu_budget):
                          "bytes_per_launch": nbytes, "kernel": "causal_conv1d_step_kernel"}}
 
 
+def bench_decode_fused(dev, steps, warmup, cpu_budget):
+    """Fused decode step (conv update + L2 norm + gating + recurrent step), and
+    the same step as the separate ops in the reference's dtype flow."""
+    import torch.nn.functional as F
+
+    from myvllm_amd import causal_conv1d_update, gated_delta_net_decode_step, recurrent_gated_delta_rule
+    from myvllm_amd.workloads import CONV_WIDTH, decode_fused_case
+
+    B, slots = 256, 1024
+    D = 2 * HK * DK + HV * DV
+    case = decode_fused_case(B=B, num_slots=slots, seed=0, state=False)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    state = torch.randn(slots, HV, DK, DV, device=dev, generator=gen) * 0.1
+    perm = torch.randperm(slots, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    idxs = [perm[i * B:(i + 1) * B].to(dev) for i in range(4)]
+    x, w, cs, a, b, A_log, dt_bias = (t.to(dev) for t in (case.mixed_qkv, case.conv_weight, case.conv_state, case.a,
+                                                          case.b, case.A_log, case.dt_bias))
+
+    def step(i):
+        gated_delta_net_decode_step(x, w, cs, idxs[i % 4], a, b, A_log, dt_bias, state, idxs[i % 4], HK)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+
+    def separate(i):  # layers/linear_attention.py:89-90, :95, :97-114, :119 as separate ops
+        beta = b.sigmoid()
+        g = -A_log.float().exp() * F.softplus(a.float() + dt_bias)
+        y = causal_conv1d_update(x, w, cs, idxs[i % 4])
+        q, k, v = torch.split(y, [HK * DK, HK * DK, HV * DV], dim=-1)
+        q, k, v = q.reshape(B, HK, DK), k.reshape(B, HK, DK), v.reshape(B, HV, DV)
+        q = q * torch.rsqrt(q.pow(2).sum(dim=-1, keepdim=True) + 1e-6)
+        k = k * torch.rsqrt(k.pow(2).sum(dim=-1, keepdim=True) + 1e-6)
+        recurrent_gated_delta_rule(q, k, v, g, beta, state, idxs[i % 4])
+
+    ms_sep, _ = _time_gpu(separate, steps, warmup)
+    per_seq = 2 * HV * DK * DV * 4 + 2 * (CONV_WIDTH - 1) * D * 4 + D * 2 + HV * DV * 2 + 2 * HV * 2
+    nbytes = per_seq * B + D * CONV_WIDTH * 2 + 2 * HV * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+            "separate_ops_ms_per_step": ms_sep,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("gdn_decode_fused_kernel"),
+                         "bytes_per_launch": nbytes, "kernel": "gdn_decode_fused_kernel"}}
+
+
 def bench_hbm_copy(dev, steps, warmup, cpu_budget):
     """Plain 1 GiB device-to-device copy: the calibration point of the HBM
     byte counters and the copy bandwidth this device reaches."""
@@ -260,7 +306,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update", "hbm_copy"], default="all")
+    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update", "decode_fused", "hbm_copy"],
+                    default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     args = ap.parse_args()
@@ -289,6 +336,11 @@ def main():
     if want("conv_update"):
         parts["conv_update"] = bench_conv_update(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# conv_update: {parts['conv_update']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if want("decode_fused"):
+        parts["decode_fused"] = bench_decode_fused(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# decode_fused: {parts['decode_fused']['kernel_ms'] * 1e3:.1f} us/launch "
+              f"(separate ops: {parts['decode_fused']['separate_ops_ms_per_step'] * 1e3:.1f} us/step)",
+              file=sys.stderr, flush=True)
     if args.workload == "hbm_copy":
         parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
 
@@ -301,6 +353,10 @@ def main():
     elif head_name == "decode":
         metric, value, unit = "GDN decode state-update HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "gdn_recurrent_step: batch 256 from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128"
+    elif head_name == "decode_fused":
+        metric, value, unit = "GDN fused decode step HBM GB/s", head["GB_per_s"], "GB/s"
+        workload = ("gdn_decode_step_fused: batch 256, conv update (8192 channels, width 4, fp32 conv state) + "
+                    "L2 norm + gating + recurrent step from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128")
     elif head_name == "hbm_copy":
         metric, value, unit = "device copy HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "hbm_copy: 1 GiB device-to-device copy (read + write counted)"

@@ -24,6 +24,10 @@
  *                            ops/gated_delta_rule/gated_delta_rule.py:31-66
  *  - causal_conv1d_varlen <- causal_conv1d_fn, ops/causal_conv1d.py:221-273
  *  - causal_conv1d_step   <- causal_conv1d_update, ops/causal_conv1d.py:434-470
+ *  - gdn_decode_step_fused <- the decode branch of GatedDeltaNet.forward,
+ *                            layers/linear_attention.py:89-90 (gating), :95
+ *                            (causal_conv1d_update), :113-114 (L2 norm), :119
+ *                            (recurrent_gated_delta_rule), one launch instead of four
  */
 #ifndef GDN_HIP_H_
 #define GDN_HIP_H_
@@ -131,6 +135,33 @@ int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weight, gdn_tens
  */
 int causal_conv1d_step(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
                        const gdn_tensor* conv_state_indices, gdn_tensor* out, void* stream);
+
+/*
+ * One decode token of a whole GDN layer's recurrent part, fused: replaces
+ * the decode branch of GatedDeltaNet.forward (layers/linear_attention.py:95
+ * causal_conv1d_update -> :113-114 per-head L2 norm of q, k -> :89-90 gating
+ * -> :119 recurrent_gated_delta_rule).
+ *   mixed_qkv   (B, D) the projections before the conv, D = 2 Hk K + Hv V,
+ *               channels q (Hk K) | k (Hk K) | v (Hv V); out has its dtype
+ *   conv_weight (D, 4); conv_state (conv_slots, 3, D); conv_state_indices (B,)
+ *   a, b        (B, Hv) gate and beta inputs; A_log, dt_bias (Hv,)
+ *   state       (slots, Hv, K, V) fp32, K = V = 128; state_indices (B,)
+ *   out         (B, Hv, V)
+ * Per sequence: xt = [conv_state[cslot]; mixed_qkv_b], y = silu(sum_j w[:, j] xt[j]),
+ * conv_state[cslot] <- xt[1:]; q, k, v = split(y); q, k <- x rsqrt(sum x^2 + 1e-6)
+ * per head; g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b); then the
+ * gated delta rule step of gdn_recurrent_step with scale.  The conv output,
+ * the normalised q, k and the gates stay in fp32 (no rounding to the input
+ * dtype between the steps).  A padding conv slot gives a zero conv output
+ * (as causal_conv1d_step does); a padding state slot gives a zero output row
+ * and leaves the state untouched; the two caches are indexed independently.
+ * Hv / Hk must be 1, 2 or 4; both caches need at least one slot when B > 0.
+ */
+int gdn_decode_step_fused(const gdn_tensor* mixed_qkv, const gdn_tensor* conv_weight, gdn_tensor* conv_state,
+                          const gdn_tensor* conv_state_indices, const gdn_tensor* a, const gdn_tensor* b,
+                          const gdn_tensor* A_log, const gdn_tensor* dt_bias, gdn_tensor* state,
+                          const gdn_tensor* state_indices, gdn_tensor* out, int32_t num_k_heads, float scale,
+                          void* stream);
 
 /* Text for any return code of this library. */
 const char* gdn_strerror(int code);

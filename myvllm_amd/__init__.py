@@ -7,6 +7,7 @@ from .causal_conv1d import causal_conv1d_fn, causal_conv1d_update
 from .gated_delta_rule import (
     chunk_gated_delta_rule,
     chunk_gated_delta_rule_fwd,
+    gated_delta_net_decode_step,
     recurrent_gated_delta_rule,
 )
 
@@ -15,5 +16,6 @@ __all__ = [
     "causal_conv1d_update",
     "chunk_gated_delta_rule",
     "chunk_gated_delta_rule_fwd",
+    "gated_delta_net_decode_step",
     "recurrent_gated_delta_rule",
 ]

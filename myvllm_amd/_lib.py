@@ -29,6 +29,7 @@ EXPORTED_SYMBOLS = (
     "gdn_chunk_prefill",
     "causal_conv1d_varlen",
     "causal_conv1d_step",
+    "gdn_decode_step_fused",
     "gdn_strerror",
     "gdn_abi_version",
 )
@@ -85,6 +86,8 @@ def load() -> ctypes.CDLL:
         lib.causal_conv1d_varlen.argtypes = [_PT] * 6 + [ctypes.c_void_p]
         lib.causal_conv1d_step.restype = ctypes.c_int
         lib.causal_conv1d_step.argtypes = [_PT] * 5 + [ctypes.c_void_p]
+        lib.gdn_decode_step_fused.restype = ctypes.c_int
+        lib.gdn_decode_step_fused.argtypes = [_PT] * 11 + [ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]
         if lib.gdn_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI {lib.gdn_abi_version()}, expected {ABI_VERSION}; rebuild it")
         _lib = lib

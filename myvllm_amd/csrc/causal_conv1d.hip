@@ -31,14 +31,7 @@ struct ConvArgs {
   bool idx64, cu64;
 };
 
-// Taps are held pre-multiplied by -log2(e), so a convolution gives
-// a = -log2(e) * acc directly, and
-//   silu(acc) = acc / (1 + e^-acc) = a / (-log2(e) * (1 + 2^a)),
-// one exp2, one fma, one reciprocal and one multiply per element.
-constexpr float kNegLog2e = -1.4426950408889634f;
-GDN_DEVICE float silu_from_scaled(float a) {
-  return a * __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(a), kNegLog2e, kNegLog2e));
-}
+// Taps are held pre-multiplied by -log2(e) (silu_from_scaled, gdn_common.h).
 GDN_DEVICE void scale_taps(float (*wr)[kCh], int W) {
   for (int j = 0; j < W; ++j)
 #pragma unroll

@@ -21,6 +21,10 @@ hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w,
                                        hipStream_t st);
 hipError_t causal_conv1d_step_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                      const gdn_tensor* idx, gdn_tensor* out, hipStream_t st);
+hipError_t gdn_decode_fused_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs, const gdn_tensor* cidx,
+                                   const gdn_tensor* ga, const gdn_tensor* gb, const gdn_tensor* A_log,
+                                   const gdn_tensor* dt_bias, gdn_tensor* state, const gdn_tensor* sidx,
+                                   gdn_tensor* out, int32_t Hk, float scale, hipStream_t st);
 
 #define GDN_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -181,6 +185,52 @@ int check_conv(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, c
   return GDN_OK;
 }
 
+int check_fused(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, const gdn_tensor* cidx,
+                const gdn_tensor* ga, const gdn_tensor* gb, const gdn_tensor* A_log, const gdn_tensor* dt_bias,
+                const gdn_tensor* state, const gdn_tensor* sidx, const gdn_tensor* out, int32_t Hk) {
+  GDN_TRY(check_desc(x, 2));
+  GDN_TRY(check_desc(w, 2));
+  GDN_TRY(check_desc(cs, 3));
+  GDN_TRY(check_desc(cidx, 1));
+  GDN_TRY(check_desc(ga, 2));
+  GDN_TRY(check_desc(gb, 2));
+  GDN_TRY(check_desc(A_log, 1));
+  GDN_TRY(check_desc(dt_bias, 1));
+  GDN_TRY(check_desc(state, 4));
+  GDN_TRY(check_desc(sidx, 1));
+  GDN_TRY(check_desc(out, 3));
+
+  const int64_t B = x->shape[0], D = x->shape[1];
+  const int64_t Hv = state->shape[1], K = state->shape[2], V = state->shape[3];
+  if (w->shape[1] != 4) return GDN_ERR_CONV_WIDTH;
+  if (K != 128 || V != 128) return GDN_ERR_HEAD_DIM;
+  if (Hk <= 0 || Hv % Hk != 0) return GDN_ERR_HEADS;
+  const int64_t r = Hv / Hk;
+  if (r != 1 && r != 2 && r != 4) return GDN_ERR_HEADS;
+  if (D != 2 * Hk * K + Hv * V) return GDN_ERR_SHAPE;
+  if (w->shape[0] != D || cs->shape[1] != 3 || cs->shape[2] != D) return GDN_ERR_SHAPE;
+  if (cidx->shape[0] != B || sidx->shape[0] != B) return GDN_ERR_SHAPE;
+  if (ga->shape[0] != B || ga->shape[1] != Hv || gb->shape[0] != B || gb->shape[1] != Hv) return GDN_ERR_SHAPE;
+  if (A_log->shape[0] != Hv || dt_bias->shape[0] != Hv) return GDN_ERR_SHAPE;
+  if (out->shape[0] != B || out->shape[1] != Hv || out->shape[2] != V) return GDN_ERR_SHAPE;
+  // padding rows still read slot 0 of each cache (branch-free loads), so a
+  // non-empty batch needs a non-empty cache
+  if (B > 0 && (cs->shape[0] < 1 || state->shape[0] < 1)) return GDN_ERR_SHAPE;
+
+  if (!is_float(x->dtype) || out->dtype != x->dtype) return GDN_ERR_DTYPE;
+  if (!is_float(w->dtype) || !is_float(cs->dtype) || !is_float(ga->dtype) || !is_float(gb->dtype) ||
+      !is_float(A_log->dtype) || !is_float(dt_bias->dtype))
+    return GDN_ERR_DTYPE;
+  if (state->dtype != GDN_DTYPE_F32 || !is_index(cidx->dtype) || !is_index(sidx->dtype)) return GDN_ERR_DTYPE;
+
+  if (x->stride[1] != 1 || cs->stride[2] != 1 || out->stride[2] != 1) return GDN_ERR_STRIDE;
+  if (state->stride[3] != 1 || state->stride[2] != V) return GDN_ERR_STRIDE;
+  if (cidx->stride[0] != 1 || sidx->stride[0] != 1) return GDN_ERR_STRIDE;
+  if (B > 0 && !vec_ok(state, 16)) return GDN_ERR_ALIGN;
+  if (B * Hk > kMaxGrid) return GDN_ERR_RANGE;
+  return GDN_OK;
+}
+
 int launch_rc(hipError_t e) { return e == hipSuccess ? GDN_OK : (int)e; }
 
 }  // namespace
@@ -238,4 +288,16 @@ GDN_EXPORT int causal_conv1d_step(const gdn_tensor* x, const gdn_tensor* weight,
   GDN_TRY(check_conv(x, weight, conv_state, conv_state_indices, nullptr, out, false));
   return launch_rc(causal_conv1d_step_launch(x, weight, conv_state, conv_state_indices, out,
                                              reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_decode_step_fused(const gdn_tensor* mixed_qkv, const gdn_tensor* conv_weight,
+                                     gdn_tensor* conv_state, const gdn_tensor* conv_state_indices,
+                                     const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log,
+                                     const gdn_tensor* dt_bias, gdn_tensor* state, const gdn_tensor* state_indices,
+                                     gdn_tensor* out, int32_t num_k_heads, float scale, void* stream) {
+  GDN_TRY(check_fused(mixed_qkv, conv_weight, conv_state, conv_state_indices, a, b, A_log, dt_bias, state,
+                      state_indices, out, num_k_heads));
+  return launch_rc(gdn_decode_fused_launch(mixed_qkv, conv_weight, conv_state, conv_state_indices, a, b, A_log,
+                                           dt_bias, state, state_indices, out, num_k_heads, scale,
+                                           reinterpret_cast<hipStream_t>(stream)));
 }

@@ -139,6 +139,16 @@ GDN_DEVICE float scalar_raw_f32(ScalarRaw r, int dtype) {
   return __builtin_bit_cast(float, (r.hi << 16) | r.lo);
 }
 
+// ---- SiLU of a convolution with pre-scaled taps --------------------------
+// With the taps held pre-multiplied by -log2(e), a convolution gives
+// a = -log2(e) * acc directly, and
+//   silu(acc) = acc / (1 + e^-acc) = a / (-log2(e) * (1 + 2^a)),
+// one exp2, one fma, one reciprocal and one multiply per element.
+constexpr float kNegLog2e = -1.4426950408889634f;
+GDN_DEVICE float silu_from_scaled(float a) {
+  return a * __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(a), kNegLog2e, kNegLog2e));
+}
+
 // ---- index tensors (int32 or int64) ----------------------------------------
 GDN_DEVICE int64_t load_index(const void* p, int64_t i, bool is64) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];

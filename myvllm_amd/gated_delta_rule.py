@@ -108,3 +108,43 @@ def chunk_gated_delta_rule_fwd(
     idx = torch.arange(N, dtype=torch.int32, device=v.device)
     o = chunk_gated_delta_rule(q, k, v, g, beta, cache, idx, cu_seqlens, scale=scale)
     return o, (cache if output_final_state else None)
+
+
+def gated_delta_net_decode_step(
+    mixed_qkv: torch.Tensor,  # (B, 2 Hk K + Hv V): the qkv projection before the conv
+    conv_weight: torch.Tensor,  # (D, 4)
+    conv_state: torch.Tensor,  # (conv_slots, 3, D)
+    conv_state_indices: torch.Tensor,  # (B,)
+    a: torch.Tensor,  # (B, Hv) gate input
+    b: torch.Tensor,  # (B, Hv) beta input
+    A_log: torch.Tensor,  # (Hv,)
+    dt_bias: torch.Tensor,  # (Hv,)
+    recurrent_state: torch.Tensor,  # (slots, Hv, K, V) fp32
+    recurrent_state_indices: torch.Tensor,  # (B,)
+    num_k_heads: int,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """The decode branch of ``GatedDeltaNet.forward`` in one launch (reference
+    ``layers/linear_attention.py:89-90`` gating, ``:95`` ``causal_conv1d_update``,
+    ``:113-114`` per-head L2 norm of q and k, ``:119`` ``recurrent_gated_delta_rule``).
+
+    Returns o (B, Hv, V) in ``mixed_qkv``'s dtype and updates both caches in
+    place.  The conv output, the normalised q and k and the gates stay in fp32
+    between the steps (the separate ops round them to the input dtype).
+    """
+    dev = _lib.require_device(mixed_qkv, conv_weight, conv_state, conv_state_indices, a, b, A_log, dt_bias,
+                              recurrent_state, recurrent_state_indices)
+    mixed_qkv = _lastdim_contiguous(mixed_qkv)
+    Hv, K, V = recurrent_state.shape[1], recurrent_state.shape[2], recurrent_state.shape[3]
+    if scale is None:
+        scale = K ** -0.5
+    o = torch.empty((mixed_qkv.shape[0], Hv, V), dtype=mixed_qkv.dtype, device=dev)
+    lib = _lib.load()
+    D = _lib.describe
+    rc = lib.gdn_decode_step_fused(
+        D(mixed_qkv), D(conv_weight), D(conv_state), D(conv_state_indices), D(a), D(b), D(A_log), D(dt_bias),
+        D(recurrent_state), D(recurrent_state_indices), D(o), int(num_k_heads), float(scale),
+        _lib.stream_handle(dev),
+    )
+    _lib.check("gdn_decode_step_fused", rc)
+    return o

@@ -151,3 +151,42 @@ def conv_decode_case(B: int = 256, seed: int = 0, D: int = CONV_DIM, W: int = CO
     st = (torch.randn(num_slots, W - 1, D, generator=gen) * 0.02).to(dtype).to(state_dtype)
     idx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
     return ConvCase(x, w, st, idx, None)
+
+
+@dataclass
+class FusedDecodeCase:
+    mixed_qkv: torch.Tensor  # (B, 2 Hk K + Hv V)
+    conv_weight: torch.Tensor  # (D, 4)
+    conv_state: torch.Tensor  # (conv_slots, 3, D)
+    conv_idx: torch.Tensor  # (B,)
+    a: torch.Tensor  # (B, Hv)
+    b: torch.Tensor  # (B, Hv)
+    A_log: torch.Tensor  # (Hv,)
+    dt_bias: torch.Tensor  # (Hv,)
+    state: torch.Tensor | None  # (slots, Hv, K, V) fp32
+    idx: torch.Tensor  # (B,)
+    Hk: int
+
+
+def decode_fused_case(B: int = 256, num_slots: int = 1024, seed: int = 0, Hk: int = HK, Hv: int = HV,
+                      K: int = DK, V: int = DV, dtype=torch.bfloat16, conv_state_dtype=torch.float32,
+                      weight_dtype=None, state: bool = True) -> FusedDecodeCase:
+    """Fused decode workload (conv update + L2 norm + gating + recurrent step):
+    B sequences x 1 token of the packed q|k|v projections ~N(0, 1), conv taps
+    ~N(0, 0.3), conv state ~N(0, 1), a, b ~N(0, 1) in ``dtype``,
+    A_log = log U(1, 16), dt_bias = 1 (the layer's initialisation), fp32
+    recurrent state ~N(0, 0.1); the conv and recurrent caches have
+    ``num_slots`` slots each and are indexed by independent permutations."""
+    gen = torch.Generator().manual_seed(seed)
+    D = 2 * Hk * K + Hv * V
+    x = torch.randn(B, D, generator=gen).to(dtype)
+    w = (torch.randn(D, CONV_WIDTH, generator=gen) * 0.3).to(weight_dtype or dtype)
+    cs = torch.randn(num_slots, CONV_WIDTH - 1, D, generator=gen).to(dtype).to(conv_state_dtype)
+    a = torch.randn(B, Hv, generator=gen).to(dtype)
+    b = torch.randn(B, Hv, generator=gen).to(dtype)
+    A_log = torch.log(torch.rand(Hv, generator=gen) * 15 + 1)
+    dt_bias = torch.ones(Hv)
+    cidx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
+    idx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
+    st = torch.randn(num_slots, Hv, K, V, generator=gen) * 0.1 if state else None
+    return FusedDecodeCase(x, w, cs, cidx, a, b, A_log, dt_bias, st, idx, Hk)

@@ -4,15 +4,27 @@
   (``layers/linear_attention.py:89-90``);
 * per-head L2 norm: x * rsqrt(sum x^2 + 1e-6) (``layers/linear_attention.py:113-114``);
 * gated RMSNorm: x * rsqrt(mean x^2 + eps) * w * silu(gate), fp32 math, output in
-  x's dtype (``layers/norm.py:50-58``).
+  x's dtype (``layers/norm.py:50-58``);
+* the decode branch of the layer as one step: conv update, split, L2 norm,
+  gating, recurrent step (``layers/linear_attention.py:89-90``, ``:95``,
+  ``:97-114``, ``:119``), composed from the restatements above and in
+  ``oracle.conv`` / ``oracle.gdn``.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
 
+from .conv import causal_conv1d_update_ref
+from .gdn import recurrent_gated_delta_rule_ref
 
-def gdn_gating_ref(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor):
+
+def gdn_gating_ref(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
+                   dtype: torch.dtype | None = None):
+    """g, beta as the layer forms them; ``dtype`` (e.g. fp64) evaluates the same
+    formulas in that dtype instead of the layer's fp32 / b-dtype mix."""
+    if dtype is not None:
+        return -A_log.to(dtype).exp() * F.softplus(a.to(dtype) + dt_bias.to(dtype)), b.to(dtype).sigmoid()
     beta = b.sigmoid()
     g = -A_log.float().exp() * F.softplus(a.float() + dt_bias)
     return g, beta
@@ -28,3 +40,21 @@ def rms_norm_gated_ref(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor
     var = xf.pow(2).mean(dim=-1, keepdim=True) + eps
     y = xf * var.rsqrt() * weight.float() * F.silu(gate.float())
     return y.to(dt)
+
+
+def gdn_decode_step_ref(mixed_qkv, conv_weight, conv_state, conv_state_indices, a, b, A_log, dt_bias,
+                        recurrent_state, recurrent_state_indices, num_k_heads, scale=None):
+    """One decode token of the layer's recurrent part, in fp64 with no rounding
+    between the pieces; mutates both caches, returns o (B, Hv, V) in
+    ``mixed_qkv``'s dtype."""
+    B = mixed_qkv.shape[0]
+    Hv, K, V = recurrent_state.shape[1], recurrent_state.shape[2], recurrent_state.shape[3]
+    Hk = num_k_heads
+    y = causal_conv1d_update_ref(mixed_qkv.double(), conv_weight, conv_state, conv_state_indices)  # fp64
+    q, k, v = torch.split(y, [Hk * K, Hk * K, Hv * V], dim=-1)
+    q = l2norm_ref(q.reshape(B, Hk, K))
+    k = l2norm_ref(k.reshape(B, Hk, K))
+    v = v.reshape(B, Hv, V)
+    g, beta = gdn_gating_ref(a, b, A_log, dt_bias, dtype=torch.float64)
+    o = recurrent_gated_delta_rule_ref(q, k, v, g, beta, recurrent_state, recurrent_state_indices, scale=scale)
+    return o.to(mixed_qkv.dtype)

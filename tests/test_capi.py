@@ -169,6 +169,60 @@ def test_conv_step_validation():
     assert rc == ERR["SHAPE"]  # 3 tokens, 2 slot indices
 
 
+def _fused_args(B=2, Hk=2, Hv=4, K=128, V=128, slots=3, dtype=torch.bfloat16):
+    Dc = 2 * Hk * K + Hv * V
+    return dict(
+        x=torch.zeros(B, Dc, dtype=dtype), w=torch.zeros(Dc, 4, dtype=dtype), cs=torch.zeros(slots, 3, Dc),
+        cidx=torch.zeros(B, dtype=torch.int32), a=torch.zeros(B, Hv, dtype=dtype), b=torch.zeros(B, Hv, dtype=dtype),
+        A_log=torch.zeros(Hv), dt_bias=torch.zeros(Hv), state=torch.zeros(slots, Hv, K, V),
+        idx=torch.zeros(B, dtype=torch.int32), out=torch.zeros(B, Hv, V, dtype=dtype), Hk=Hk,
+    )
+
+
+def _call_fused(a):
+    lib = _lib.load()
+    return lib.gdn_decode_step_fused(D(a["x"]), D(a["w"]), D(a["cs"]), D(a["cidx"]), D(a["a"]), D(a["b"]),
+                                     D(a["A_log"]), D(a["dt_bias"]), D(a["state"]), D(a["idx"]), D(a["out"]),
+                                     a["Hk"], 0.1, None)
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "mutate,code",
+    [
+        (lambda a: a.update(w=torch.zeros(1024, 3, dtype=torch.bfloat16)), "CONV_WIDTH"),
+        (lambda a: a.update(Hk=3), "HEADS"),
+        (lambda a: a.update(Hk=0), "HEADS"),
+        (lambda a: a.update(x=torch.zeros(2, 1000, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(cs=torch.zeros(3, 2, 1024)), "SHAPE"),
+        (lambda a: a.update(cs=torch.zeros(0, 3, 1024)), "SHAPE"),
+        (lambda a: a.update(state=torch.zeros(0, 4, 128, 128)), "SHAPE"),
+        (lambda a: a.update(cidx=torch.zeros(3, dtype=torch.int32)), "SHAPE"),
+        (lambda a: a.update(a=torch.zeros(2, 3, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(A_log=torch.zeros(5)), "SHAPE"),
+        (lambda a: a.update(out=torch.zeros(2, 4, 128)), "DTYPE"),
+        (lambda a: a.update(state=torch.zeros(3, 4, 128, 128, dtype=torch.float16)), "DTYPE"),
+        (lambda a: a.update(idx=torch.zeros(2, dtype=torch.float32)), "DTYPE"),
+        (lambda a: a.update(state=torch.zeros(3, 4, 64, 64), x=torch.zeros(2, 512, dtype=torch.bfloat16),
+                            w=torch.zeros(512, 4, dtype=torch.bfloat16), cs=torch.zeros(3, 3, 512),
+                            out=torch.zeros(2, 4, 64, dtype=torch.bfloat16)), "HEAD_DIM"),
+        (lambda a: a.update(x=torch.zeros(1024, 2, dtype=torch.bfloat16).t()), "STRIDE"),
+        (lambda a: a.update(cidx=torch.zeros(4, dtype=torch.int32)[::2]), "STRIDE"),
+        (lambda a: a.update(state=torch.zeros(3 * 4 * 128 * 128 + 1)[1:].view(3, 4, 128, 128)), "ALIGN"),
+    ],
+)
+def test_fused_decode_validation(mutate, code):
+    a = _fused_args()
+    mutate(a)
+    assert _call_fused(a) == ERR[code]
+
+
+@cpu_only
+def test_fused_decode_heads_ratio_eight_rejected():
+    a = _fused_args(Hk=1, Hv=8)
+    assert _call_fused(a) == ERR["HEADS"]
+
+
 def test_ops_reject_cpu_tensors():
     from myvllm_amd import causal_conv1d_update, recurrent_gated_delta_rule
 
