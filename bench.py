@@ -282,6 +282,76 @@ def bench_decode_fused(dev, steps, warmup, cpu_budget):
                          "bytes_per_launch": nbytes, "kernel": "gdn_decode_fused_kernel"}}
 
 
+def bench_layer(dev, steps, warmup, cpu_budget):
+    """The full GDN layer (hidden 2048, Hk 16 / Hv 32, d 128) on a mixed batch of
+    4 x 2048 prefill tokens and 128 decode tokens, with a per-stage breakdown."""
+    from myvllm_amd import causal_conv1d_fn, chunk_gated_delta_rule, gated_delta_net_decode_step
+    from myvllm_amd.cache import LinearAttentionCache
+    from myvllm_amd.layer import GatedDeltaNet
+    from myvllm_amd.norm import gdn_gating, rms_norm_gated
+    from myvllm_amd.workloads import cu_from_lengths
+
+    hidden, n_pre, len_pre, n_dec = 2048, 4, 2048, 128
+    layer = GatedDeltaNet(hidden, HK, HV, DK, DV, device=dev)
+    layer.init_random(std=0.02, seed=0)
+    cache = LinearAttentionCache(1, n_pre + n_dec, 4, DK, DV, HK, HV, torch.bfloat16, dev, conv_dtype=torch.float32)
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    slots = torch.tensor([cache.allocate() for _ in range(n_pre + n_dec)], dtype=torch.int32, device=dev)
+    T = n_pre * len_pre + n_dec
+    x = torch.randn(T, hidden, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    cu = cu_from_lengths([len_pre] * n_pre).to(dev)
+
+    def step(_):
+        layer(x, cu, slots, slots, num_decode_tokens=n_dec)
+
+    ms, _ = _time_gpu(step, steps, warmup)
+
+    # the same forward, stage by stage, with events between the stages
+    Tp, Np, L = n_pre * len_pre, n_pre, layer
+    names = ["in_proj GEMM", "conv + q/k L2 norm", "gating", "chunked prefill", "fused decode step",
+             "gated RMSNorm", "out_proj GEMM"]
+    cz = L.conv_dim + L.v_size
+    acc = [0.0] * len(names)
+    stream = torch.cuda.current_stream()
+    for it in range(warmup + steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        ev[0].record(stream)
+        proj = x @ L.in_proj.t()
+        ev[1].record(stream)
+        qkv, z = proj[:, :L.conv_dim], proj[:, L.conv_dim:cz]
+        b, a = proj[:, cz:cz + HV], proj[:, cz + HV:]
+        y = causal_conv1d_fn(qkv[:Tp], L.conv1d_weight, L.conv_state, slots[:Np], cu, l2norm_channels=2 * L.k_size)
+        ev[2].record(stream)
+        g, beta = gdn_gating(a[:Tp], b[:Tp], L.A_log, L.dt_bias)
+        ev[3].record(stream)
+        o = torch.empty(T, HV, DV, dtype=x.dtype, device=dev)
+        chunk_gated_delta_rule(y[:, :L.k_size].view(Tp, HK, DK), y[:, L.k_size:2 * L.k_size].view(Tp, HK, DK),
+                               y[:, 2 * L.k_size:].view(Tp, HV, DV), g, beta, L.recurrent_state, slots[:Np], cu,
+                               out=o[:Tp])
+        ev[4].record(stream)
+        gated_delta_net_decode_step(qkv[Tp:], L.conv1d_weight, L.conv_state, slots[Np:], a[Tp:], b[Tp:], L.A_log,
+                                    L.dt_bias, L.recurrent_state, slots[Np:], HK, out=o[Tp:])
+        ev[5].record(stream)
+        on = rms_norm_gated(o, z.view(T, HV, DV), L.norm_weight, L.rms_norm_eps)
+        ev[6].record(stream)
+        on.view(T, L.v_size) @ L.out_proj.t()
+        ev[7].record(stream)
+        torch.cuda.synchronize()
+        if it >= warmup:
+            for i in range(len(names)):
+                acc[i] += ev[i].elapsed_time(ev[i + 1]) / steps
+    gemm_flop = 2 * T * hidden * (L.conv_dim + L.v_size + 2 * HV) + 2 * T * L.v_size * hidden
+    gdn_flop = PREFILL_FLOP_PER_TOKEN * Tp
+    flop = gemm_flop + gdn_flop
+    achieved = flop / (ms * 1e-3) / 1e12
+    return {"tokens": T, "prefill_tokens": Tp, "decode_tokens": n_dec, "ms_per_step": ms, "kernel_ms": ms,
+            "tokens_per_s": T / (ms * 1e-3),
+            "stages_ms": {n: round(v, 4) for n, v in zip(names, acc)},
+            "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                         "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": None, "flop_per_launch": flop,
+                         "kernel": "whole layer (GEMMs + GDN prefill FLOPs over the step time)"}}
+
+
 def bench_hbm_copy(dev, steps, warmup, cpu_budget):
     """Plain 1 GiB device-to-device copy: the calibration point of the HBM
     byte counters and the copy bandwidth this device reaches."""
@@ -306,7 +376,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["all", "prefill", "decode", "conv", "conv_update", "decode_fused", "hbm_copy"],
+    ap.add_argument("--workload",
+                    choices=["all", "prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "hbm_copy"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
@@ -341,6 +412,12 @@ def main():
         print(f"# decode_fused: {parts['decode_fused']['kernel_ms'] * 1e3:.1f} us/launch "
               f"(separate ops: {parts['decode_fused']['separate_ops_ms_per_step'] * 1e3:.1f} us/step)",
               file=sys.stderr, flush=True)
+    if want("layer"):
+        parts["layer"] = bench_layer(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# layer: {parts['layer']['ms_per_step'] * 1e3:.1f} us/step "
+              f"({parts['layer']['tokens_per_s'] / 1e6:.2f} M tokens/s); stages (us): "
+              + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in parts["layer"]["stages_ms"].items()),
+              file=sys.stderr, flush=True)
     if args.workload == "hbm_copy":
         parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
 
@@ -357,6 +434,10 @@ def main():
         metric, value, unit = "GDN fused decode step HBM GB/s", head["GB_per_s"], "GB/s"
         workload = ("gdn_decode_step_fused: batch 256, conv update (8192 channels, width 4, fp32 conv state) + "
                     "L2 norm + gating + recurrent step from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128")
+    elif head_name == "layer":
+        metric, value, unit = "GDN layer tokens/s", head["tokens_per_s"], "tokens/s"
+        workload = ("GatedDeltaNet layer: hidden 2048, Hk 16 / Hv 32, d 128, conv 4; 4 x 2048 prefill + 128 decode "
+                    "tokens in one call, bf16 weights ~N(0, 0.02), fp32 states")
     elif head_name == "hbm_copy":
         metric, value, unit = "device copy HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "hbm_copy: 1 GiB device-to-device copy (read + write counted)"

@@ -24,6 +24,11 @@
  *                            ops/gated_delta_rule/gated_delta_rule.py:31-66
  *  - causal_conv1d_varlen <- causal_conv1d_fn, ops/causal_conv1d.py:221-273
  *  - causal_conv1d_step   <- causal_conv1d_update, ops/causal_conv1d.py:434-470
+ *  - gdn_rms_norm_gated   <- RMSNormGated, layers/norm.py:44-58
+ *  - gdn_gating           <- the gates of GatedDeltaNet.forward,
+ *                            layers/linear_attention.py:89-90
+ *  - causal_conv1d_varlen_qknorm <- causal_conv1d_fn + the L2 norm of
+ *                            layers/linear_attention.py:113-114, one launch
  *  - gdn_decode_step_fused <- the decode branch of GatedDeltaNet.forward,
  *                            layers/linear_attention.py:89-90 (gating), :95
  *                            (causal_conv1d_update), :113-114 (L2 norm), :119
@@ -162,6 +167,37 @@ int gdn_decode_step_fused(const gdn_tensor* mixed_qkv, const gdn_tensor* conv_we
                           const gdn_tensor* A_log, const gdn_tensor* dt_bias, gdn_tensor* state,
                           const gdn_tensor* state_indices, gdn_tensor* out, int32_t num_k_heads, float scale,
                           void* stream);
+
+/*
+ * causal_conv1d_varlen, and the per-head L2 norm of the layer
+ * (layers/linear_attention.py:113-114, y * rsqrt(sum y^2 + 1e-6) over each
+ * 128-channel head) applied in fp32 to output channels [0, norm_channels)
+ * before the one rounding to x's dtype: the q and k of the packed q|k|v
+ * projection, normalised in the conv's epilogue.  norm_channels: a multiple
+ * of 128, at most D.  No counterpart in the reference as one op.
+ */
+int causal_conv1d_varlen_qknorm(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                                const gdn_tensor* conv_state_indices, const gdn_tensor* cu_seqlens,
+                                gdn_tensor* out, int64_t norm_channels, void* stream);
+
+/*
+ * Gated RMSNorm of the GDN output <- RMSNormGated, layers/norm.py:44-58 (applied
+ * per v-head at layers/linear_attention.py:121):
+ *   out = x * rsqrt(mean(x^2) + eps) * weight * silu(gate), fp32 math.
+ * x, gate, out: (T, H, 128), same dtype, unit inner stride, 16-byte aligned
+ * rows; weight: (128,) fp32, bf16 or fp16.
+ */
+int gdn_rms_norm_gated(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* weight, gdn_tensor* out,
+                       float eps, void* stream);
+
+/*
+ * The layer's gates <- layers/linear_attention.py:89-90:
+ *   g = -exp(A_log) * softplus(a + dt_bias),  beta = sigmoid(b),  fp32 math.
+ * a, b: (T, H) fp32|bf16|fp16, unit inner stride; A_log, dt_bias: (H,);
+ * g, beta: (T, H) fp32 outputs.
+ */
+int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log, const gdn_tensor* dt_bias,
+               gdn_tensor* g, gdn_tensor* beta, void* stream);
 
 /* Text for any return code of this library. */
 const char* gdn_strerror(int code);

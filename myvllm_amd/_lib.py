@@ -30,6 +30,9 @@ EXPORTED_SYMBOLS = (
     "causal_conv1d_varlen",
     "causal_conv1d_step",
     "gdn_decode_step_fused",
+    "causal_conv1d_varlen_qknorm",
+    "gdn_rms_norm_gated",
+    "gdn_gating",
     "gdn_strerror",
     "gdn_abi_version",
 )
@@ -88,6 +91,12 @@ def load() -> ctypes.CDLL:
         lib.causal_conv1d_step.argtypes = [_PT] * 5 + [ctypes.c_void_p]
         lib.gdn_decode_step_fused.restype = ctypes.c_int
         lib.gdn_decode_step_fused.argtypes = [_PT] * 11 + [ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]
+        lib.causal_conv1d_varlen_qknorm.restype = ctypes.c_int
+        lib.causal_conv1d_varlen_qknorm.argtypes = [_PT] * 6 + [ctypes.c_int64, ctypes.c_void_p]
+        lib.gdn_rms_norm_gated.restype = ctypes.c_int
+        lib.gdn_rms_norm_gated.argtypes = [_PT] * 4 + [ctypes.c_float, ctypes.c_void_p]
+        lib.gdn_gating.restype = ctypes.c_int
+        lib.gdn_gating.argtypes = [_PT] * 6 + [ctypes.c_void_p]
         if lib.gdn_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI {lib.gdn_abi_version()}, expected {ABI_VERSION}; rebuild it")
         _lib = lib

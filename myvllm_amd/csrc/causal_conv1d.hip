@@ -28,6 +28,7 @@ struct ConvArgs {
   const void* x; const void* w; void* state; const void* idx; const void* cu; void* out;
   int64_t x_s0, w_s0, w_s1, st_s0, st_s1, o_s0;
   int64_t T, D, nseq, num_slots;
+  int64_t norm_ch;  // channels [0, norm_ch) are L2-normalised per 128-channel head (0: none)
   bool idx64, cu64;
 };
 
@@ -131,6 +132,18 @@ GDN_DEVICE void conv_tile(const ConvArgs& a, int64_t seq, int64_t tile, int64_t 
 #pragma unroll
         for (int m = 0; m < W - 1; ++m) acc = fmaf(wr[m][c], win[m][c], acc);
         y[c] = silu_from_scaled(acc);
+      }
+      if (a.norm_ch > 0) {
+        // per-head L2 norm x rsqrt(sum x^2 + 1e-6) of the q and k channels
+        // (layers/linear_attention.py:113-114): a head's 128 channels are the
+        // 8 channels of 16 consecutive lanes, one DPP row
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < kCh; ++c) ss = fmaf(y[c], y[c], ss);
+        ss = row16_sum(ss);
+        const float sc = d0 < a.norm_ch ? rsqrtf(ss + 1e-6f) : 1.f;
+#pragma unroll
+        for (int c = 0; c < kCh; ++c) y[c] *= sc;
       }
       if (r0 + u < nt)
         Vec8<TX>::store(reinterpret_cast<TX*>(reinterpret_cast<char*>(ot) + (uint32_t)(r0 + u) * os * (uint32_t)sizeof(TX)), y);
@@ -256,8 +269,9 @@ hipError_t launch_weight(bool varlen, const ConvArgs& a, int wdt, int sdt, int W
 }
 
 hipError_t launch_conv(bool varlen, const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
-                       const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, hipStream_t st) {
+                       const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, int64_t norm_ch, hipStream_t st) {
   ConvArgs a;
+  a.norm_ch = norm_ch;
   a.x = x->data; a.w = w->data; a.state = cs->data; a.idx = idx->data;
   a.cu = cu ? cu->data : nullptr; a.out = out->data;
   a.x_s0 = x->stride[0]; a.w_s0 = w->stride[0]; a.w_s1 = w->stride[1];
@@ -288,11 +302,11 @@ hipError_t launch_conv(bool varlen, const gdn_tensor* x, const gdn_tensor* w, gd
 
 hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
-                                       hipStream_t st) {
-  return launch_conv(true, x, w, cs, idx, cu, out, st);
+                                       int64_t norm_ch, hipStream_t st) {
+  return launch_conv(true, x, w, cs, idx, cu, out, norm_ch, st);
 }
 
 hipError_t causal_conv1d_step_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                      const gdn_tensor* idx, gdn_tensor* out, hipStream_t st) {
-  return launch_conv(false, x, w, cs, idx, nullptr, out, st);
+  return launch_conv(false, x, w, cs, idx, nullptr, out, 0, st);
 }

@@ -18,7 +18,11 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
                                     hipStream_t st);
 hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
-                                       hipStream_t st);
+                                       int64_t norm_ch, hipStream_t st);
+hipError_t gdn_rms_norm_gated_launch(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* w,
+                                     gdn_tensor* out, float eps, hipStream_t st);
+hipError_t gdn_gating_launch(const gdn_tensor* ga, const gdn_tensor* gb, const gdn_tensor* A_log,
+                             const gdn_tensor* dt_bias, gdn_tensor* g, gdn_tensor* beta, hipStream_t st);
 hipError_t causal_conv1d_step_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                      const gdn_tensor* idx, gdn_tensor* out, hipStream_t st);
 hipError_t gdn_decode_fused_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs, const gdn_tensor* cidx,
@@ -279,7 +283,7 @@ GDN_EXPORT int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weigh
                                     const gdn_tensor* conv_state_indices, const gdn_tensor* cu_seqlens,
                                     gdn_tensor* out, void* stream) {
   GDN_TRY(check_conv(x, weight, conv_state, conv_state_indices, cu_seqlens, out, true));
-  return launch_rc(causal_conv1d_varlen_launch(x, weight, conv_state, conv_state_indices, cu_seqlens, out,
+  return launch_rc(causal_conv1d_varlen_launch(x, weight, conv_state, conv_state_indices, cu_seqlens, out, 0,
                                                reinterpret_cast<hipStream_t>(stream)));
 }
 
@@ -300,4 +304,54 @@ GDN_EXPORT int gdn_decode_step_fused(const gdn_tensor* mixed_qkv, const gdn_tens
   return launch_rc(gdn_decode_fused_launch(mixed_qkv, conv_weight, conv_state, conv_state_indices, a, b, A_log,
                                            dt_bias, state, state_indices, out, num_k_heads, scale,
                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int causal_conv1d_varlen_qknorm(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,
+                                           const gdn_tensor* conv_state_indices, const gdn_tensor* cu_seqlens,
+                                           gdn_tensor* out, int64_t norm_channels, void* stream) {
+  GDN_TRY(check_conv(x, weight, conv_state, conv_state_indices, cu_seqlens, out, true));
+  if (norm_channels < 0 || norm_channels % 128 != 0 || norm_channels > x->shape[1]) return GDN_ERR_SHAPE;
+  return launch_rc(causal_conv1d_varlen_launch(x, weight, conv_state, conv_state_indices, cu_seqlens, out,
+                                               norm_channels, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_rms_norm_gated(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* weight,
+                                  gdn_tensor* out, float eps, void* stream) {
+  GDN_TRY(check_desc(x, 3));
+  GDN_TRY(check_desc(gate, 3));
+  GDN_TRY(check_desc(weight, 1));
+  GDN_TRY(check_desc(out, 3));
+  for (int i = 0; i < 3; ++i)
+    if (gate->shape[i] != x->shape[i] || out->shape[i] != x->shape[i]) return GDN_ERR_SHAPE;
+  if (weight->shape[0] != x->shape[2]) return GDN_ERR_SHAPE;
+  if (x->shape[2] != 128) return GDN_ERR_HEAD_DIM;
+  if (!is_float(x->dtype) || out->dtype != x->dtype || gate->dtype != x->dtype || !is_float(weight->dtype))
+    return GDN_ERR_DTYPE;
+  if (x->stride[2] != 1 || gate->stride[2] != 1 || out->stride[2] != 1 || weight->stride[0] != 1)
+    return GDN_ERR_STRIDE;
+  if (numel(x) > 0 && (!vec_ok(x, 16) || !vec_ok(gate, 16) || !vec_ok(out, 16))) return GDN_ERR_ALIGN;
+  if (x->shape[0] * x->shape[1] > kMaxGrid * 16) return GDN_ERR_RANGE;
+  return launch_rc(gdn_rms_norm_gated_launch(x, gate, weight, out, eps, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log, const gdn_tensor* dt_bias,
+                          gdn_tensor* g, gdn_tensor* beta, void* stream) {
+  GDN_TRY(check_desc(a, 2));
+  GDN_TRY(check_desc(b, 2));
+  GDN_TRY(check_desc(A_log, 1));
+  GDN_TRY(check_desc(dt_bias, 1));
+  GDN_TRY(check_desc(g, 2));
+  GDN_TRY(check_desc(beta, 2));
+  const int64_t T = a->shape[0], H = a->shape[1];
+  if (b->shape[0] != T || b->shape[1] != H || g->shape[0] != T || g->shape[1] != H || beta->shape[0] != T ||
+      beta->shape[1] != H || A_log->shape[0] != H || dt_bias->shape[0] != H)
+    return GDN_ERR_SHAPE;
+  if (!is_float(a->dtype) || !is_float(b->dtype) || !is_float(A_log->dtype) || !is_float(dt_bias->dtype))
+    return GDN_ERR_DTYPE;
+  if (g->dtype != GDN_DTYPE_F32 || beta->dtype != GDN_DTYPE_F32) return GDN_ERR_DTYPE;
+  if (a->stride[1] != 1 || b->stride[1] != 1 || g->stride[1] != 1 || beta->stride[1] != 1 ||
+      A_log->stride[0] != 1 || dt_bias->stride[0] != 1)
+    return GDN_ERR_STRIDE;
+  if (T * H > kMaxGrid) return GDN_ERR_RANGE;
+  return launch_rc(gdn_gating_launch(a, b, A_log, dt_bias, g, beta, reinterpret_cast<hipStream_t>(stream)));
 }

@@ -165,6 +165,20 @@ GDN_DEVICE void seq_range(const void* cu, bool cu64, int64_t n, int64_t T, int64
 }
 
 
+// Sum over the 16 lanes of a DPP row, on every lane of the row (quad swaps,
+// then the half-row and row mirrors).
+template <int CTRL>
+GDN_DEVICE float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+GDN_DEVICE float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  return x;
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the
 // row broadcasts of the last lane of each row).
 GDN_DEVICE int wave_inclusive_scan_i32(int x) {

@@ -37,15 +37,17 @@ def chunk_gated_delta_rule(
     recurrent_state_indices: torch.Tensor,  # (seq_cnt,)
     cu_seqlens: torch.Tensor,  # (seq_cnt + 1,)
     scale: float | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Prefill over packed varlen sequences (reference ``gated_delta_rule.py:31-66``)."""
+    """Prefill over packed varlen sequences (reference ``gated_delta_rule.py:31-66``);
+    ``out`` (optional) receives o in place of a new tensor."""
     dev = _lib.require_device(q, k, v, g, beta, recurrent_state, recurrent_state_indices, cu_seqlens)
     q, k, v = _lastdim_contiguous(q), _lastdim_contiguous(k), _lastdim_contiguous(v)
     if g.dtype != torch.float32:
         g = g.float()
     if scale is None:
         scale = k.shape[-1] ** -0.5
-    o = torch.empty(v.shape, dtype=v.dtype, device=dev)
+    o = torch.empty(v.shape, dtype=v.dtype, device=dev) if out is None else out
     lib = _lib.load()
     D = _lib.describe
     rc = lib.gdn_chunk_prefill(
@@ -123,6 +125,7 @@ def gated_delta_net_decode_step(
     recurrent_state_indices: torch.Tensor,  # (B,)
     num_k_heads: int,
     scale: float | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The decode branch of ``GatedDeltaNet.forward`` in one launch (reference
     ``layers/linear_attention.py:89-90`` gating, ``:95`` ``causal_conv1d_update``,
@@ -138,7 +141,7 @@ def gated_delta_net_decode_step(
     Hv, K, V = recurrent_state.shape[1], recurrent_state.shape[2], recurrent_state.shape[3]
     if scale is None:
         scale = K ** -0.5
-    o = torch.empty((mixed_qkv.shape[0], Hv, V), dtype=mixed_qkv.dtype, device=dev)
+    o = torch.empty((mixed_qkv.shape[0], Hv, V), dtype=mixed_qkv.dtype, device=dev) if out is None else out
     lib = _lib.load()
     D = _lib.describe
     rc = lib.gdn_decode_step_fused(

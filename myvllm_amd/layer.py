@@ -1,0 +1,113 @@
+"""The Gated DeltaNet layer around the hot path, on one MI355X.
+
+Replaces ``GatedDeltaNet`` (``layers/linear_attention.py:15-124`` of
+yuyifanbupt/myvllm) with the intended dataflow of its ``forward`` (the
+reference convolves ``x`` instead of the qkv projection, norms with the
+wrong shapes and projects ``z``, ``:93``, ``:95``, ``:121-122``):
+
+  qkv | z = x W_qkvz^T ;  b | a = x W_ba^T                      (:85-88)
+  g = -exp(A_log) softplus(a + dt_bias),  beta = sigmoid(b)     (:89-90)
+  prefill tokens: y = causal_conv1d(qkv) with the per-head L2 norm of q, k
+                  fused into its epilogue (:93, :97-114), then
+                  o = chunk_gated_delta_rule(q, k, v, g, beta)   (:117)
+  decode tokens:  o = gated_delta_net_decode_step(qkv, a, b)     (:95-119 in one launch)
+  o = RMSNormGated(o, z) per v-head                              (:121)
+  out = o W_out^T                                                (:122)
+
+The four input projections are one GEMM (rows q|k|v|z|b|a; measured faster
+than separate q|k|v|z and b|a GEMMs on this device) and every GEMM is
+torch's (hipBLASLt); the gates are one small kernel.  One call takes a mixed batch: the prefill
+sequences' tokens first (``cu_seqlens`` covers them), then
+``num_decode_tokens`` decode tokens, one per sequence, whose slot ids follow
+the prefill ones in the index tensors (the reference takes one
+``is_prefill`` flag per call, ``:83``, ``:92``, ``:116``).  Single GPU: the
+tensor-parallel head split (``:28-38``) is one GPU's share.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+
+from .causal_conv1d import causal_conv1d_fn
+from .gated_delta_rule import chunk_gated_delta_rule, gated_delta_net_decode_step
+from .norm import gdn_gating, rms_norm_gated
+
+
+class GatedDeltaNet(nn.Module):
+    def __init__(
+        self,
+        hidden_size: int,
+        num_k_heads: int,
+        num_v_heads: int,
+        k_head_dim: int,
+        v_head_dim: int,
+        conv_kernel_size: int = 4,
+        rms_norm_eps: float = 1e-6,
+        dtype: torch.dtype = torch.bfloat16,
+        device: torch.device | str | None = None,
+    ) -> None:
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_k_heads = num_k_heads
+        self.num_v_heads = num_v_heads
+        self.k_head_dim = k_head_dim
+        self.v_head_dim = v_head_dim
+        self.conv_kernel_size = conv_kernel_size
+        self.rms_norm_eps = rms_norm_eps
+        self.k_size = num_k_heads * k_head_dim
+        self.v_size = num_v_heads * v_head_dim
+        self.conv_dim = 2 * self.k_size + self.v_size
+        kw = dict(dtype=dtype, device=device)
+        # rows: q | k | v | z | b | a
+        self.in_proj = nn.Parameter(torch.empty(self.conv_dim + self.v_size + 2 * num_v_heads, hidden_size, **kw))
+        self.conv1d_weight = nn.Parameter(torch.empty(self.conv_dim, conv_kernel_size, **kw))
+        self.dt_bias = nn.Parameter(torch.ones(num_v_heads, device=device))
+        self.A_log = nn.Parameter(torch.log(torch.empty(num_v_heads, device=device).uniform_(1, 16)))
+        self.norm_weight = nn.Parameter(torch.ones(v_head_dim, device=device))
+        self.out_proj = nn.Parameter(torch.empty(hidden_size, self.v_size, **kw))
+        # caches of this layer (views of a LinearAttentionCache), set by the caller as in the reference (:74-75)
+        self.conv_state: torch.Tensor = torch.empty(0)
+        self.recurrent_state: torch.Tensor = torch.empty(0)
+
+    @torch.no_grad()
+    def init_random(self, std: float = 0.02, seed: int = 0) -> None:
+        """Random-init weights ~N(0, std) (conv taps ~N(0, 1/W)), seeded on the CPU."""
+        gen = torch.Generator().manual_seed(seed)
+        for p, s in ((self.in_proj, std), (self.out_proj, std),
+                     (self.conv1d_weight, 1.0 / math.sqrt(self.conv_kernel_size))):
+            p.copy_((torch.randn(p.shape, generator=gen) * s).to(p.dtype))
+
+    def forward(
+        self,
+        x: torch.Tensor,  # (T, hidden)
+        cu_seqlens: torch.Tensor,  # (N_prefill + 1,) over the first T - num_decode_tokens tokens
+        conv_state_indices: torch.Tensor,  # (N_prefill + num_decode_tokens,)
+        recurrent_state_indices: torch.Tensor,  # (N_prefill + num_decode_tokens,)
+        num_decode_tokens: int = 0,
+    ) -> torch.Tensor:
+        T = x.shape[0]
+        Tp = T - num_decode_tokens
+        Np = cu_seqlens.numel() - 1 if Tp > 0 else 0
+        Hk, Hv, K, V = self.num_k_heads, self.num_v_heads, self.k_head_dim, self.v_head_dim
+        proj = x @ self.in_proj.t()
+        cz = self.conv_dim + self.v_size
+        qkv, z = proj[:, : self.conv_dim], proj[:, self.conv_dim: cz]
+        b, a = proj[:, cz: cz + Hv], proj[:, cz + Hv:]
+        o = torch.empty(T, Hv, V, dtype=x.dtype, device=x.device)
+        if Tp > 0:
+            y = causal_conv1d_fn(qkv[:Tp], self.conv1d_weight, self.conv_state, conv_state_indices[:Np], cu_seqlens,
+                                 l2norm_channels=2 * self.k_size)
+            q = y[:, : self.k_size].view(Tp, Hk, K)
+            k = y[:, self.k_size: 2 * self.k_size].view(Tp, Hk, K)
+            v = y[:, 2 * self.k_size:].view(Tp, Hv, V)
+            g, beta = gdn_gating(a[:Tp], b[:Tp], self.A_log, self.dt_bias)
+            chunk_gated_delta_rule(q, k, v, g, beta, self.recurrent_state, recurrent_state_indices[:Np], cu_seqlens,
+                                   out=o[:Tp])
+        if num_decode_tokens > 0:
+            gated_delta_net_decode_step(
+                qkv[Tp:], self.conv1d_weight, self.conv_state, conv_state_indices[Np:], a[Tp:], b[Tp:], self.A_log,
+                self.dt_bias, self.recurrent_state, recurrent_state_indices[Np:], Hk, out=o[Tp:])
+        on = rms_norm_gated(o, z.view(T, Hv, V), self.norm_weight, self.rms_norm_eps)
+        return on.view(T, self.v_size) @ self.out_proj.t()

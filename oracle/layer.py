@@ -15,8 +15,8 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from .conv import causal_conv1d_update_ref
-from .gdn import recurrent_gated_delta_rule_ref
+from .conv import causal_conv1d_fn_ref, causal_conv1d_update_ref
+from .gdn import chunk_gated_delta_rule_ref, recurrent_gated_delta_rule_ref
 
 
 def gdn_gating_ref(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
@@ -58,3 +58,39 @@ def gdn_decode_step_ref(mixed_qkv, conv_weight, conv_state, conv_state_indices, 
     g, beta = gdn_gating_ref(a, b, A_log, dt_bias, dtype=torch.float64)
     o = recurrent_gated_delta_rule_ref(q, k, v, g, beta, recurrent_state, recurrent_state_indices, scale=scale)
     return o.to(mixed_qkv.dtype)
+
+
+def gdn_layer_ref(x, w_qkvz, w_ba, conv_weight, A_log, dt_bias, norm_weight, w_out, conv_state, conv_state_indices,
+                  recurrent_state, recurrent_state_indices, cu_seqlens, num_k_heads, num_decode_tokens=0,
+                  eps=1e-6):
+    """The layer's intended forward (``layers/linear_attention.py:85-122`` with the
+    conv on the qkv projection and the norm on o) over a mixed batch: prefill
+    tokens first (``cu_seqlens``), then ``num_decode_tokens`` single-token
+    sequences.  The projections' outputs are rounded to x's dtype, as the
+    layer's linear layers return them; everything after is fp64 except the
+    gated norm's fp32.  Mutates both caches; returns (T, hidden) in x's dtype."""
+    T = x.shape[0]
+    Hv, K, V = recurrent_state.shape[1], recurrent_state.shape[2], recurrent_state.shape[3]
+    Hk = num_k_heads
+    Dc = 2 * Hk * K + Hv * V
+    Tp = T - num_decode_tokens
+    Np = cu_seqlens.numel() - 1 if Tp > 0 else 0
+    xd = x.double()
+    qkvz = (xd @ w_qkvz.double().t()).to(x.dtype).double()
+    ba = (xd @ w_ba.double().t()).to(x.dtype).double()
+    qkv, z = qkvz[:, :Dc], qkvz[:, Dc:]
+    b, a = ba[:, :Hv], ba[:, Hv:]
+    o = torch.zeros(T, Hv, V, dtype=torch.float64)
+    if Tp > 0:
+        y = causal_conv1d_fn_ref(qkv[:Tp], conv_weight, conv_state, conv_state_indices[:Np], cu_seqlens)
+        q = l2norm_ref(y[:, : Hk * K].reshape(Tp, Hk, K))
+        k = l2norm_ref(y[:, Hk * K: 2 * Hk * K].reshape(Tp, Hk, K))
+        v = y[:, 2 * Hk * K:].reshape(Tp, Hv, V)
+        g, beta = gdn_gating_ref(a[:Tp], b[:Tp], A_log, dt_bias, dtype=torch.float64)
+        o[:Tp] = chunk_gated_delta_rule_ref(q, k, v, g, beta, recurrent_state, recurrent_state_indices[:Np],
+                                            cu_seqlens)
+    if num_decode_tokens > 0:
+        o[Tp:] = gdn_decode_step_ref(qkv[Tp:], conv_weight, conv_state, conv_state_indices[Np:], a[Tp:], b[Tp:],
+                                     A_log, dt_bias, recurrent_state, recurrent_state_indices[Np:], Hk)
+    on = rms_norm_gated_ref(o, z.reshape(T, Hv, V), norm_weight, eps=eps).double()
+    return (on.reshape(T, Hv * V) @ w_out.double().t()).to(x.dtype)
