@@ -44,10 +44,11 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_075_139_713,
-    "gdn_recurrent_step_kernel": 1_083_193_349,
-    "causal_conv1d_varlen_kernel": 665_911_711,
-    "causal_conv1d_step_kernel": 59_314_135,
+    "gdn_chunk_prefill_kernel": 1_050_890_969,
+    "gdn_recurrent_step_kernel": 1_083_200_285,
+    "causal_conv1d_varlen_kernel": 666_053_847,
+    "causal_conv1d_step_kernel": 59_313_267,
+    "gdn_decode_fused_kernel": 1_131_400_901,
 }
 
 
@@ -376,9 +377,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload",
-                    choices=["all", "prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "hbm_copy"],
-                    default="all")
+    ap.add_argument("--workload", default="all",
+                    help="all, or a comma-separated list of prefill, decode, conv, conv_update, decode_fused, "
+                         "layer, hbm_copy")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     args = ap.parse_args()
@@ -393,8 +394,13 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "hbm_copy"}
+    chosen = set(args.workload.split(","))
+    if not chosen <= (known | {"all"}):
+        print(f"unknown workload(s): {sorted(chosen - known - {'all'})}", file=sys.stderr)
+        sys.exit(2)
     parts = {}
-    want = (lambda w: args.workload in ("all", w))
+    want = (lambda w: "all" in chosen or w in chosen)
     if want("prefill"):
         parts["prefill"] = bench_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# prefill: {parts['prefill']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
@@ -418,7 +424,7 @@ def main():
               f"({parts['layer']['tokens_per_s'] / 1e6:.2f} M tokens/s); stages (us): "
               + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in parts["layer"]["stages_ms"].items()),
               file=sys.stderr, flush=True)
-    if args.workload == "hbm_copy":
+    if "hbm_copy" in chosen:
         parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
 
     head_name = "prefill" if "prefill" in parts else next(iter(parts))
