@@ -306,3 +306,44 @@ def test_workload_lengths_match_the_benchmark_description():
     assert cp().cu.diff().tolist() == [2943, 3503, 2192, 1807, 3696, 649, 3521, 1451]
     c = prefill_32k_case()
     assert c.tokens == 35846 and int(((c.cu.diff() + 63) // 64).sum()) == 567
+
+
+# ---- full-attention neighbour -------------------------------------------------------
+
+from oracle.attention import attention_loop_ref, flash_attention_prefill_ref, paged_attention_ref  # noqa: E402
+
+
+def test_attention_matches_scalar_loops_with_gqa():
+    g = torch.Generator().manual_seed(11)
+    q, k, v = torch.randn(5, 4, 3, generator=g), torch.randn(5, 2, 3, generator=g), torch.randn(5, 2, 2, generator=g)
+    for causal in (True, False):
+        o = flash_attention_prefill_ref(q, k, v, torch.tensor([0, 5]), 0.7, is_causal=causal)
+        assert torch.allclose(o.double(), attention_loop_ref(q, k, v, 0.7, torch.arange(5), causal), atol=1e-6)
+
+
+def test_attention_closed_forms():
+    g = torch.Generator().manual_seed(12)
+    v = torch.randn(6, 1, 4, generator=g, dtype=torch.float64)
+    q = torch.randn(6, 2, 8, generator=g, dtype=torch.float64)
+    k = torch.zeros(6, 1, 8, dtype=torch.float64)  # all scores equal: causal o_i = mean(v_0..v_i)
+    o = flash_attention_prefill_ref(q, k, v, torch.tensor([0, 6]), 1.0, is_causal=True)
+    means = torch.cumsum(v[:, 0], 0) / torch.arange(1, 7, dtype=torch.float64)[:, None]
+    assert torch.allclose(o[:, 0], means) and torch.allclose(o[:, 1], means)
+    assert torch.allclose(o[0, :, :], v[0, 0].expand(2, 4))  # the first token attends only to itself
+
+
+def test_paged_attention_equals_contiguous_and_permuted_pages():
+    g = torch.Generator().manual_seed(13)
+    bs, L, n = 4, 11, 3  # 11 cached keys, the last 3 are this prefill's queries
+    k = torch.randn(L, 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(L, 2, 8, generator=g, dtype=torch.float64)
+    q = torch.randn(n, 4, 8, generator=g, dtype=torch.float64)
+    table = torch.tensor([5, 1, 3])  # pages in any order
+    kc = torch.zeros(6, bs, 2, 8, dtype=torch.float64)
+    vc = torch.zeros(6, bs, 2, 8, dtype=torch.float64)
+    for j in range(L):
+        kc[table[j // bs], j % bs] = k[j]
+        vc[table[j // bs], j % bs] = v[j]
+    o = paged_attention_ref(q, kc, vc, table[None], torch.tensor([L]), torch.tensor([0, n]), 0.5)
+    ref = attention_loop_ref(q, k, v, 0.5, torch.arange(L - n, L), True)
+    assert torch.allclose(o, ref, atol=1e-9)
