@@ -33,6 +33,9 @@
  *                            layers/linear_attention.py:89-90 (gating), :95
  *                            (causal_conv1d_update), :113-114 (L2 norm), :119
  *                            (recurrent_gated_delta_rule), one launch instead of four
+ *  - flash_attention_varlen  <- flash_attention_prefill, ops/full_attention.py:114-173
+ *  - paged_attention_prefill <- paged_flash_attention_prefill, ops/full_attention.py:454-512
+ *  - paged_attention_decode  <- paged_flash_attention_decode, ops/full_attention.py:282-335
  */
 #ifndef GDN_HIP_H_
 #define GDN_HIP_H_
@@ -198,6 +201,52 @@ int gdn_rms_norm_gated(const gdn_tensor* x, const gdn_tensor* gate, const gdn_te
  */
 int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log, const gdn_tensor* dt_bias,
                gdn_tensor* g, gdn_tensor* beta, void* stream);
+
+/*
+ * Full attention of the hybrid stack's attention layers (GQA: query head h
+ * reads kv head h / (Hq / Hkv)); bf16 or fp16 throughout, fp32 softmax, P
+ * rounded to the input dtype before P V.  Head dim D = 64, 128 or 256 (the
+ * same for q, k and v); unit inner strides and 16-byte aligned rows.
+ *
+ * flash_attention_varlen <- flash_attention_prefill, ops/full_attention.py:114-173
+ *   q (T, Hq, D), k, v (T, Hkv, D), out (T, Hq, D), cu_seqlens (N+1,).
+ *   Per sequence, query i attends keys 0..i (causal != 0) or all the
+ *   sequence's keys.  max_seqlen must be at least the longest sequence
+ *   (rows past it are left unwritten).
+ */
+int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                           const gdn_tensor* cu_seqlens, gdn_tensor* out, int64_t max_seqlen, float scale,
+                           int32_t causal, void* stream);
+
+/*
+ * paged_attention_prefill <- paged_flash_attention_prefill, ops/full_attention.py:454-512
+ *   q, out (T, Hq, D); k_cache, v_cache (num_blocks, page, Hkv, D);
+ *   block_tables (N, max_blocks) i32|i64; context_lens (N,); cu_seqlens (N+1,).
+ *   Query i of sequence n sits at position context_lens[n] - len_n + i and
+ *   attends causally to cached keys 0..position, key j at slot j % page of
+ *   block block_tables[n][j / page].  A query with no visible key gives a
+ *   zero row; table entries outside [0, num_blocks) read as zero keys (never
+ *   out of bounds).  The reference's block_m_indices work list is not needed.
+ */
+int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                            const gdn_tensor* block_tables, const gdn_tensor* context_lens,
+                            const gdn_tensor* cu_seqlens, gdn_tensor* out, int64_t max_seqlen, float scale,
+                            void* stream);
+
+/*
+ * paged_attention_decode <- paged_flash_attention_decode, ops/full_attention.py:282-335
+ *   q, out (B, Hq, D): one query per sequence, at position context_lens[b] - 1;
+ *   caches and block_tables (B, max_blocks) as above.  The keys of a sequence
+ *   are split into num_splits ranges (1..256) merged by a second launch; with
+ *   num_splits > 1, workspace is an fp32 1-D tensor of at least
+ *   paged_attention_decode_workspace_size(B, Hq, D, num_splits) elements
+ *   (16-byte aligned), overwritten.  context_lens[b] = 0 gives a zero row.
+ */
+int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim,
+                                              int32_t num_splits);
+int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                           const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
+                           gdn_tensor* workspace, int32_t num_splits, float scale, void* stream);
 
 /* Text for any return code of this library. */
 const char* gdn_strerror(int code);

@@ -33,6 +33,10 @@ EXPORTED_SYMBOLS = (
     "causal_conv1d_varlen_qknorm",
     "gdn_rms_norm_gated",
     "gdn_gating",
+    "flash_attention_varlen",
+    "paged_attention_prefill",
+    "paged_attention_decode_workspace_size",
+    "paged_attention_decode",
     "gdn_strerror",
     "gdn_abi_version",
 )
@@ -97,6 +101,16 @@ def load() -> ctypes.CDLL:
         lib.gdn_rms_norm_gated.argtypes = [_PT] * 4 + [ctypes.c_float, ctypes.c_void_p]
         lib.gdn_gating.restype = ctypes.c_int
         lib.gdn_gating.argtypes = [_PT] * 6 + [ctypes.c_void_p]
+        lib.flash_attention_varlen.restype = ctypes.c_int
+        lib.flash_attention_varlen.argtypes = [_PT] * 5 + [ctypes.c_int64, ctypes.c_float, ctypes.c_int32,
+                                                           ctypes.c_void_p]
+        lib.paged_attention_prefill.restype = ctypes.c_int
+        lib.paged_attention_prefill.argtypes = [_PT] * 7 + [ctypes.c_int64, ctypes.c_float, ctypes.c_void_p]
+        lib.paged_attention_decode_workspace_size.restype = ctypes.c_int64
+        lib.paged_attention_decode_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                                              ctypes.c_int32]
+        lib.paged_attention_decode.restype = ctypes.c_int
+        lib.paged_attention_decode.argtypes = [_PT] * 7 + [ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]
         if lib.gdn_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI {lib.gdn_abi_version()}, expected {ABI_VERSION}; rebuild it")
         _lib = lib

@@ -19,7 +19,15 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIBNAME = "libgdn_hip.so"
-SOURCES = ["gdn_decode.hip", "gdn_decode_fused.hip", "gdn_prefill.hip", "causal_conv1d.hip", "gdn_norm.hip", "gdn_capi.cpp"]
+SOURCES = [
+    "gdn_decode.hip",
+    "gdn_decode_fused.hip",
+    "gdn_prefill.hip",
+    "causal_conv1d.hip",
+    "gdn_norm.hip",
+    "attention.hip",
+    "gdn_capi.cpp",
+]
 
 ARCH = "gfx950"
 # Packed-FP32 VALU ops are disabled for all device code (they are generated

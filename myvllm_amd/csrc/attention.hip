@@ -1,0 +1,634 @@
+// Full-attention kernels of the hybrid stack for gfx950: varlen and paged
+// prefill on 32x32x16 MFMA tiles, split-KV paged decode on 16x16 tiles.
+//
+// Reference: ops/full_attention.py of yuyifanbupt/myvllm (flash_attention_prefill
+// :114-173, paged_flash_attention_decode :282-335, paged_flash_attention_prefill
+// :454-512).  Query head h reads kv head h / (Hq / Hkv); softmax in fp32 with a
+// running maximum; P rounded to the input dtype before P V, the row sum taken
+// over the unrounded fp32 P (:100-107).
+//
+// Layout of the prefill tile: the score tile is computed transposed,
+// S^T = K Q^T, so that lane l of a wave owns query column l % 32 of the
+// accumulator.  The softmax statistics of a query then live in one lane pair
+// (l, l ^ 32), and the exponentiated accumulator registers are already the B
+// operand of O^T = V^T P^T, whose A operand is read from the row-major V tile
+// with ds_read_b64_tr_b16.  The running maximum is re-based only when a new
+// tile raises it by more than 2^8 (in exp2 units); O and the row sum always
+// share the same base, so the result is the same softmax.
+#include "gdn_common.h"
+
+namespace {
+
+template <typename T> struct Mma;
+template <> struct Mma<bf16_t> {
+  typedef bf16x8 v8;
+  typedef bf16x4 v4;
+  static GDN_DEVICE f32x16 m32(v8 a, v8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+  static GDN_DEVICE f32x4 m16k32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+  static GDN_DEVICE f32x4 m16k16(v4 a, v4 b, f32x4 c) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mma<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  static GDN_DEVICE f32x16 m32(v8 a, v8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+  static GDN_DEVICE f32x4 m16k32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+  static GDN_DEVICE f32x4 m16k16(v4 a, v4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+};
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short __attribute__((address_space(3))) lds_short;
+typedef s16x4_t __attribute__((address_space(3))) lds_s16x4_t;
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane i supplies the address of
+// 4 consecutive 16-bit elements of row (i >> 2), columns 4 (i & 3) .. +3, of
+// a 4 x 16 block, and receives column i of that block (rows 0..3).
+template <typename V4> GDN_DEVICE V4 tr4(const void* p) {
+  return __builtin_bit_cast(V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p)));
+}
+
+GDN_DEVICE float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+GDN_DEVICE int64_t clamp64(int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); }
+
+// Row j of a key or value source: packed varlen rows (row s0 + j) or paged
+// rows (block table[n][j / page], slot j % page).  nullptr past the valid
+// range or for a table entry outside [0, num_blocks): such rows read as zero.
+struct KvSource {
+  const char* base;
+  int64_t sb, st, sh;  // byte strides: block (paged), row, head
+};
+
+struct PagedTable {
+  const void* table;
+  int64_t row_stride, cols, num_blocks;
+  int32_t page;
+  bool is64;
+};
+
+struct AttnArgs {
+  const void* q;
+  int64_t q_st, q_sh;  // element strides: token, head
+  KvSource k, v;
+  void* o;
+  int64_t o_st, o_sh;
+  const void* cu;
+  const void* ctx;
+  PagedTable tab;
+  int64_t T;
+  int32_t Hq, Hkv, gh;  // gh: query heads per workgroup (1, 2 or 4)
+  float c;              // softmax scale * log2(e)
+  bool cu64, ctx64, causal;
+};
+
+template <bool PAGED>
+GDN_DEVICE const char* kv_row(const KvSource& s, const PagedTable& tb, int64_t n, int64_t s0, int64_t j, int kvh) {
+  if (PAGED) {
+    const int64_t col = j / tb.page;
+    if (col >= tb.cols) return nullptr;
+    const int64_t blk = load_index(tb.table, n * tb.row_stride + col, tb.is64);
+    if (blk < 0 || blk >= tb.num_blocks) return nullptr;
+    return s.base + blk * s.sb + (j - col * tb.page) * s.st + kvh * s.sh;
+  } else {
+    return s.base + (s0 + j) * s.st + kvh * s.sh;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: one workgroup = 4 waves = `gh` query heads of one kv head x
+// (4 / gh) blocks of 32 queries.  K and V tiles of BN keys are staged in LDS
+// (double buffered, the next tile prefetched into registers) and shared by
+// the four waves.
+template <typename T, int D, int BN, bool PAGED>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
+  typedef Mma<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  constexpr int LDK = D + 8;   // row stride (elements): 16-byte row skew for the b128 reads
+  constexpr int LDV = D + 32;  // 64-byte row skew for the transposed reads
+  constexpr int NKS = D / 16;
+  constexpr int NA = BN / 32;
+  constexpr int NDT = D / 32;
+  constexpr int CH = D / 8;  // 16-byte chunks per row
+  constexpr int NLD = BN * CH / 256;
+  static_assert(BN % 32 == 0 && (BN * CH) % 256 == 0, "tile");
+  __shared__ __align__(16) T ks[2][BN * LDK];
+  __shared__ __align__(16) T vs[2][BN * LDV];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t n = blockIdx.z;
+  const int R = a.Hq / a.Hkv, gh = a.gh, qsubs = 4 / gh, groups = R / gh;
+  const int kvh = blockIdx.y / groups;
+  const int head = kvh * R + (blockIdx.y % groups) * gh + (w % gh);
+
+  int64_t s0, s1;
+  seq_range(a.cu, a.cu64, n, a.T, s0, s1);
+  const int64_t len = s1 - s0;
+  const int64_t qb = (int64_t)(gridDim.x - 1 - blockIdx.x) * 32 * qsubs;  // last query blocks first
+  if (qb >= len) return;
+
+  int64_t Lk, off;
+  if (PAGED) {
+    const int64_t ctx = load_index(a.ctx, n, a.ctx64);
+    Lk = clamp64(ctx, 0, a.tab.cols * a.tab.page);
+    off = ctx - len;  // position of query 0
+  } else {
+    Lk = len;
+    off = 0;
+  }
+  const int64_t q0 = qb + (w / gh) * 32;
+  const int64_t wg_qend = qb + 32 * qsubs < len ? qb + 32 * qsubs : len;
+  const int64_t w_qend = q0 + 32 < len ? q0 + 32 : len;
+  const int64_t kend = a.causal ? clamp64(off + wg_qend, 0, Lk) : Lk;
+  const int64_t kend_w = q0 >= len ? 0 : (a.causal ? clamp64(off + w_qend, 0, Lk) : Lk);
+  const int ntiles = (int)((kend + BN - 1) / BN);
+
+  // query fragments (B operand of S^T = K Q^T): lane holds query q0 + lane % 32,
+  // dims 16 ks + 8 (lane / 32) .. +7
+  const int col = lane & 31, hh = lane >> 5;
+  const int64_t qi = q0 + col;
+  const bool qvalid = qi < len;
+  v8 qf[NKS];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q) + (s0 + (qvalid ? qi : 0)) * a.q_st + (int64_t)head * a.q_sh + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      qf[s] = qvalid ? *reinterpret_cast<const v8*>(qp + 16 * s) : v8{};
+    }
+  }
+
+  uint4 kr[NLD], vr[NLD];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int c = tid + 256 * i, row = c / CH, ch = c % CH;
+      const int64_t j = (int64_t)t * BN + row;
+      const char* pk = j < kend ? kv_row<PAGED>(a.k, a.tab, n, s0, j, kvh) : nullptr;
+      const char* pv = j < kend ? kv_row<PAGED>(a.v, a.tab, n, s0, j, kvh) : nullptr;
+      kr[i] = pk ? *reinterpret_cast<const uint4*>(pk + 16 * ch) : uint4{0, 0, 0, 0};
+      vr[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int c = tid + 256 * i, row = c / CH, ch = c % CH;
+      *reinterpret_cast<uint4*>(&ks[buf][row * LDK + 8 * ch]) = kr[i];
+      *reinterpret_cast<uint4*>(&vs[buf][row * LDV + 8 * ch]) = vr[i];
+    }
+  };
+
+  f32x16 oacc[NDT];
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) oacc[d] = f32x16{};
+  float m_used = -INFINITY, lsum = 0.f;
+  const float c = a.c;
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    if ((int64_t)t * BN < kend_w) {
+      const T* K = ks[buf];
+      const T* V = vs[buf];
+      f32x16 s[NA];
+#pragma unroll
+      for (int aa = 0; aa < NA; ++aa) {
+        s[aa] = f32x16{};
+        const T* kp = K + (32 * aa + col) * LDK + 8 * hh;
+#pragma unroll
+        for (int k = 0; k < NKS; ++k) s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), qf[k], s[aa]);
+      }
+      // mask keys past the sequence / context and, if causal, past the query
+      const int64_t tk0 = (int64_t)t * BN;
+      if (tk0 + BN > Lk || (a.causal && tk0 + BN - 1 > off + q0)) {
+        const int64_t lim = a.causal ? (off + qi + 1 < Lk ? off + qi + 1 : Lk) : Lk;
+#pragma unroll
+        for (int aa = 0; aa < NA; ++aa)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t j = tk0 + 32 * aa + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (j >= lim) s[aa][r] = -INFINITY;
+          }
+      }
+      // tile maximum of the scaled scores (c may have either sign)
+      float mt = -INFINITY;
+      if (c >= 0.f) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int aa = 0; aa < NA; ++aa)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[aa][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mt = mx == -INFINITY ? -INFINITY : mx * c;
+      } else {
+        float mn = INFINITY;
+#pragma unroll
+        for (int aa = 0; aa < NA; ++aa)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mn = s[aa][r] == -INFINITY ? mn : fminf(mn, s[aa][r]);
+        mn = fminf(mn, __shfl_xor(mn, 32));
+        mt = mn == INFINITY ? -INFINITY : mn * c;
+      }
+      if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
+        const float mn = fmaxf(m_used, mt);
+        const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
+#pragma unroll
+        for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
+        lsum *= alpha;
+        m_used = mn;
+      }
+      const float nb = m_used == -INFINITY ? 0.f : -m_used;
+#pragma unroll
+      for (int aa = 0; aa < NA; ++aa) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          v8 pf;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float sv = s[aa][8 * h2 + e];
+            const float p = sv == -INFINITY ? 0.f : exp2_fast(__builtin_fmaf(sv, c, nb));
+            lsum += p;
+            pf[e] = (T)p;
+          }
+          // V^T fragment for keys 32 aa + 16 h2 + {4 hh + 0..3, 8 + 4 hh + 0..3}
+          const int j16 = lane & 15, qd = lane >> 4;
+          const T* vp = V + (32 * aa + 16 * h2 + 4 * (qd >> 1) + (j16 >> 2)) * LDV + 16 * (qd & 1) + 4 * (j16 & 3);
+#pragma unroll
+          for (int d = 0; d < NDT; ++d) {
+            const v4 lo = tr4<v4>(vp + 32 * d);
+            const v4 hi = tr4<v4>(vp + 32 * d + 8 * LDV);
+            const v8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            oacc[d] = M::m32(vf, pf, oacc[d]);
+          }
+        }
+      }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float lt = lsum + __shfl_xor(lsum, 32);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (qvalid) {
+    T* op = reinterpret_cast<T*>(a.o) + (s0 + qi) * a.o_st + (int64_t)head * a.o_sh + 4 * hh;
+#pragma unroll
+    for (int d = 0; d < NDT; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        v4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (T)(oacc[d][4 * g + e] * inv);
+        *reinterpret_cast<v4*>(op + 32 * d + 8 * g) = ov;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Paged decode: one wave per (sequence, kv head, group of up to 16 query
+// heads, key split).  The query heads of one kv head are the 16 columns of
+// S^T = K Q^T (16x16x32 MFMA, K fragments straight from global memory), the
+// V tile goes through a wave-private LDS tile for the transposed read of
+// O^T = V^T P^T (16x16x16 MFMA).  With more than one split the wave writes
+// its unnormalised O, running maximum and row sum to the workspace and
+// attn_decode_combine_kernel merges the splits.
+struct DecodeArgs {
+  const void* q;
+  int64_t q_ss, q_sh;
+  KvSource k, v;
+  void* o;
+  int64_t o_ss, o_sh;
+  const void* ctx;
+  PagedTable tab;
+  float* part;  // (B, Hq, splits, D + 4): O, m, l (rows padded to 16 bytes)
+  int32_t B, Hq, Hkv, splits;
+  float c;
+  bool ctx64;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_decode_kernel(const DecodeArgs a) {
+  typedef Mma<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  constexpr int LDV = D + 16;  // 32-byte row skew for the transposed reads
+  constexpr int NKS = D / 32;
+  constexpr int NDT = D / 16;
+  constexpr int CH = D / 8;
+  constexpr int NLD = 16 * CH / 64;
+  __shared__ __align__(16) T vs[16 * LDV];
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.x;
+  const int64_t b = blockIdx.z;
+  const int R = a.Hq / a.Hkv, hgroups = (R + 15) / 16;
+  const int kvh = blockIdx.y / hgroups;
+  const int hcol = (blockIdx.y % hgroups) * 16 + (lane & 15);
+  const bool hvalid = hcol < R;
+  const int head = kvh * R + (hvalid ? hcol : 0);
+  const int grp = lane >> 4;
+
+  const int64_t ctx = load_index(a.ctx, b, a.ctx64);
+  const int64_t L = clamp64(ctx, 0, a.tab.cols * a.tab.page);
+  const int64_t chunk = ((L + a.splits - 1) / a.splits + 15) / 16 * 16;
+  const int64_t k_lo = chunk * split;
+  const int64_t k_hi = k_lo + chunk < L ? k_lo + chunk : L;
+  const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
+
+  v8 qf[NKS];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_ss + (int64_t)head * a.q_sh + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) qf[s] = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
+  }
+
+  v8 kf[NKS];
+  uint4 vr[NLD];
+  auto load_tile = [&](int t, v8* kd) {
+    const int64_t j0 = k_lo + 16 * (int64_t)t;
+    {
+      const int64_t j = j0 + (lane & 15);
+      const char* pk = j < k_hi ? kv_row<true>(a.k, a.tab, b, 0, j, kvh) : nullptr;
+#pragma unroll
+      for (int s = 0; s < NKS; ++s)
+        kd[s] = pk ? *reinterpret_cast<const v8*>(pk + 2 * (32 * s + 8 * grp)) : v8{};
+    }
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+      const int64_t j = j0 + row;
+      const char* pv = j < k_hi ? kv_row<true>(a.v, a.tab, b, 0, j, kvh) : nullptr;
+      vr[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+    }
+  };
+
+  f32x4 oacc[NDT];
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) oacc[d] = f32x4{};
+  float m_used = -INFINITY, lsum = 0.f;
+  const float c = a.c;
+
+  if (ntiles > 0) load_tile(0, kf);
+  for (int t = 0; t < ntiles; ++t) {
+    // V tile t to LDS (the previous tile's transposed reads were issued
+    // earlier by this wave, and LDS operations of a wave complete in order)
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+      *reinterpret_cast<uint4*>(&vs[row * LDV + 8 * ch]) = vr[i];
+    }
+    f32x4 s = f32x4{};
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) s = M::m16k32(kf[k], qf[k], s);
+    if (t + 1 < ntiles) load_tile(t + 1, kf);
+
+    // scores: lane holds head column lane % 16, keys 4 grp + r of the tile
+    const int64_t j0 = k_lo + 16 * (int64_t)t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (j0 + 4 * grp + r >= k_hi) s[r] = -INFINITY;
+    float mt;
+    if (c >= 0.f) {
+      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mt = mx == -INFINITY ? -INFINITY : mx * c;
+    } else {
+      float mn = INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mn = s[r] == -INFINITY ? mn : fminf(mn, s[r]);
+      mn = fminf(mn, __shfl_xor(mn, 16));
+      mn = fminf(mn, __shfl_xor(mn, 32));
+      mt = mn == INFINITY ? -INFINITY : mn * c;
+    }
+    if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
+      const float mn = fmaxf(m_used, mt);
+      const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
+      lsum *= alpha;
+      m_used = mn;
+    }
+    const float nb = m_used == -INFINITY ? 0.f : -m_used;
+    v4 pf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p = s[r] == -INFINITY ? 0.f : exp2_fast(__builtin_fmaf(s[r], c, nb));
+      lsum += p;
+      pf[r] = (T)p;
+    }
+    // V^T fragments: lane holds dv 16 d + lane % 16, keys 4 grp + 0..3
+    const int j16 = lane & 15;
+    const T* vp = vs + (4 * grp + (j16 >> 2)) * LDV + 4 * (j16 & 3);
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) oacc[d] = M::m16k16(tr4<v4>(vp + 16 * d), pf, oacc[d]);
+  }
+
+  float lt = lsum + __shfl_xor(lsum, 16);
+  lt += __shfl_xor(lt, 32);
+  if (!hvalid) return;
+  if (a.splits == 1) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + 4 * grp;
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) {
+      v4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = (T)(oacc[d][e] * inv);
+      *reinterpret_cast<v4*>(op + 16 * d) = ov;
+    }
+  } else {
+    float* pp = a.part + ((b * a.Hq + head) * a.splits + split) * (int64_t)(D + 4);
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) *reinterpret_cast<f32x4*>(pp + 16 * d + 4 * grp) = oacc[d];
+    if (grp == 0) {
+      pp[D] = m_used;
+      pp[D + 1] = lt;
+    }
+  }
+}
+
+// Merge of the split partials of one (sequence, query head): 64 threads,
+// D / 64 output elements each.
+template <typename T, int D>
+__global__ __launch_bounds__(64) void attn_decode_combine_kernel(const DecodeArgs a) {
+  const int64_t bh = blockIdx.x;  // b * Hq + head
+  const int64_t b = bh / a.Hq;
+  const int head = (int)(bh % a.Hq);
+  constexpr int PS = D + 4;
+  const float* pp = a.part + bh * a.splits * (int64_t)PS;
+  float mx = -INFINITY;
+  for (int s = 0; s < a.splits; ++s) mx = fmaxf(mx, pp[s * PS + D]);
+  constexpr int E = D / 64;
+  float acc[E] = {};
+  float l = 0.f;
+  for (int s = 0; s < a.splits; ++s) {
+    const float ms = pp[s * PS + D];
+    if (ms == -INFINITY) continue;
+    const float wgt = exp2_fast(ms - mx);
+    l += wgt * pp[s * PS + D + 1];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] += wgt * pp[s * PS + E * threadIdx.x + e];
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + E * threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < E; ++e) op[e] = (T)(acc[e] * inv);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+KvSource kv_source(const gdn_tensor* t, bool paged) {
+  const int64_t es = t->dtype == GDN_DTYPE_F32 ? 4 : 2;
+  KvSource s;
+  s.base = reinterpret_cast<const char*>(t->data);
+  if (paged) {
+    s.sb = t->stride[0] * es;
+    s.st = t->stride[1] * es;
+    s.sh = t->stride[2] * es;
+  } else {
+    s.sb = 0;
+    s.st = t->stride[0] * es;
+    s.sh = t->stride[1] * es;
+  }
+  return s;
+}
+
+PagedTable paged_table(const gdn_tensor* tab, const gdn_tensor* kc) {
+  PagedTable p;
+  p.table = tab->data;
+  p.row_stride = tab->stride[0];
+  p.cols = tab->shape[1];
+  p.num_blocks = kc->shape[0];
+  p.page = (int32_t)kc->shape[1];
+  p.is64 = tab->dtype == GDN_DTYPE_I64;
+  return p;
+}
+
+template <typename T, int D, int BN, bool PAGED>
+hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hipStream_t st) {
+  const int qsubs = 4 / a.gh;
+  const int64_t qblocks = (max_len + 32 * qsubs - 1) / (32 * qsubs);
+  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)nseq);
+  hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, PAGED>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <bool PAGED>
+hipError_t launch_prefill(const AttnArgs& a, int dtype, int D, int64_t nseq, int64_t max_len, hipStream_t st) {
+  if (dtype == GDN_DTYPE_BF16) {
+    if (D == 64) return launch_prefill_t<bf16_t, 64, 64, PAGED>(a, nseq, max_len, st);
+    if (D == 128) return launch_prefill_t<bf16_t, 128, 64, PAGED>(a, nseq, max_len, st);
+    return launch_prefill_t<bf16_t, 256, 32, PAGED>(a, nseq, max_len, st);
+  }
+  if (D == 64) return launch_prefill_t<f16_t, 64, 64, PAGED>(a, nseq, max_len, st);
+  if (D == 128) return launch_prefill_t<f16_t, 128, 64, PAGED>(a, nseq, max_len, st);
+  return launch_prefill_t<f16_t, 256, 32, PAGED>(a, nseq, max_len, st);
+}
+
+int heads_per_group(int R) { return R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1); }
+
+template <typename T, int D>
+hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t st) {
+  const int hgroups = (a.Hq / a.Hkv + 15) / 16;
+  const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv * hgroups), (unsigned)a.B);
+  hipLaunchKernelGGL((attn_decode_kernel<T, D>), grid, dim3(64), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)((int64_t)a.B * a.Hq)), dim3(64), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t attn_varlen_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                      const gdn_tensor* cu, gdn_tensor* out, int64_t max_seqlen, float scale,
+                                      int causal, hipStream_t st) {
+  const int64_t nseq = cu->shape[0] - 1;
+  if (nseq <= 0 || q->shape[0] == 0 || max_seqlen <= 0) return hipSuccess;
+  AttnArgs a{};
+  a.q = q->data;
+  a.q_st = q->stride[0];
+  a.q_sh = q->stride[1];
+  a.k = kv_source(k, false);
+  a.v = kv_source(v, false);
+  a.o = out->data;
+  a.o_st = out->stride[0];
+  a.o_sh = out->stride[1];
+  a.cu = cu->data;
+  a.cu64 = cu->dtype == GDN_DTYPE_I64;
+  a.T = q->shape[0];
+  a.Hq = (int32_t)q->shape[1];
+  a.Hkv = (int32_t)k->shape[1];
+  a.gh = heads_per_group(a.Hq / a.Hkv);
+  a.c = scale * kLog2e;
+  a.causal = causal != 0;
+  return launch_prefill<false>(a, q->dtype, (int)q->shape[2], nseq, max_seqlen, st);
+}
+
+hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
+                                     const gdn_tensor* tab, const gdn_tensor* ctx, const gdn_tensor* cu,
+                                     gdn_tensor* out, int64_t max_seqlen, float scale, hipStream_t st) {
+  const int64_t nseq = cu->shape[0] - 1;
+  if (nseq <= 0 || q->shape[0] == 0 || max_seqlen <= 0) return hipSuccess;
+  AttnArgs a{};
+  a.q = q->data;
+  a.q_st = q->stride[0];
+  a.q_sh = q->stride[1];
+  a.k = kv_source(kc, true);
+  a.v = kv_source(vc, true);
+  a.o = out->data;
+  a.o_st = out->stride[0];
+  a.o_sh = out->stride[1];
+  a.cu = cu->data;
+  a.cu64 = cu->dtype == GDN_DTYPE_I64;
+  a.ctx = ctx->data;
+  a.ctx64 = ctx->dtype == GDN_DTYPE_I64;
+  a.tab = paged_table(tab, kc);
+  a.T = q->shape[0];
+  a.Hq = (int32_t)q->shape[1];
+  a.Hkv = (int32_t)kc->shape[2];
+  a.gh = heads_per_group(a.Hq / a.Hkv);
+  a.c = scale * kLog2e;
+  a.causal = true;
+  return launch_prefill<true>(a, q->dtype, (int)q->shape[2], nseq, max_seqlen, st);
+}
+
+hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
+                                    const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
+                                    int32_t splits, float scale, hipStream_t st) {
+  if (q->shape[0] == 0) return hipSuccess;
+  DecodeArgs a{};
+  a.q = q->data;
+  a.q_ss = q->stride[0];
+  a.q_sh = q->stride[1];
+  a.k = kv_source(kc, true);
+  a.v = kv_source(vc, true);
+  a.o = out->data;
+  a.o_ss = out->stride[0];
+  a.o_sh = out->stride[1];
+  a.ctx = ctx->data;
+  a.ctx64 = ctx->dtype == GDN_DTYPE_I64;
+  a.tab = paged_table(tab, kc);
+  a.part = workspace;
+  a.B = (int32_t)q->shape[0];
+  a.Hq = (int32_t)q->shape[1];
+  a.Hkv = (int32_t)kc->shape[2];
+  a.splits = splits;
+  a.c = scale * kLog2e;
+  const int D = (int)q->shape[2];
+  if (q->dtype == GDN_DTYPE_BF16) {
+    if (D == 64) return launch_decode_t<bf16_t, 64>(a, st);
+    if (D == 128) return launch_decode_t<bf16_t, 128>(a, st);
+    return launch_decode_t<bf16_t, 256>(a, st);
+  }
+  if (D == 64) return launch_decode_t<f16_t, 64>(a, st);
+  if (D == 128) return launch_decode_t<f16_t, 128>(a, st);
+  return launch_decode_t<f16_t, 256>(a, st);
+}

@@ -30,6 +30,16 @@ hipError_t gdn_decode_fused_launch(const gdn_tensor* x, const gdn_tensor* w, gdn
                                    const gdn_tensor* dt_bias, gdn_tensor* state, const gdn_tensor* sidx,
                                    gdn_tensor* out, int32_t Hk, float scale, hipStream_t st);
 
+hipError_t attn_varlen_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                      const gdn_tensor* cu, gdn_tensor* out, int64_t max_seqlen, float scale,
+                                      int causal, hipStream_t st);
+hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
+                                     const gdn_tensor* tab, const gdn_tensor* ctx, const gdn_tensor* cu,
+                                     gdn_tensor* out, int64_t max_seqlen, float scale, hipStream_t st);
+hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
+                                    const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
+                                    int32_t splits, float scale, hipStream_t st);
+
 #define GDN_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace {
@@ -237,6 +247,44 @@ int check_fused(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, 
 
 int launch_rc(hipError_t e) { return e == hipSuccess ? GDN_OK : (int)e; }
 
+constexpr int64_t kMaxGridYZ = 65535;
+constexpr int32_t kMaxDecodeSplits = 256;
+
+// q / out (rows, Hq, D) with the kv tensors' head count and head dim: bf16 or
+// fp16 throughout, D = 64, 128 or 256, unit inner strides, 16-byte rows.
+int check_attn_qo(const gdn_tensor* q, const gdn_tensor* out, const gdn_tensor* kv0, const gdn_tensor* kv1,
+                  int64_t Hkv) {
+  const int64_t rows = q->shape[0], Hq = q->shape[1], D = q->shape[2];
+  if (out->shape[0] != rows || out->shape[1] != Hq || out->shape[2] != D) return GDN_ERR_SHAPE;
+  const int kd = kv0->ndim - 1;
+  if (kv0->shape[kd] != D || kv1->shape[kd] != D) return GDN_ERR_SHAPE;
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return GDN_ERR_HEADS;
+  if (q->dtype != GDN_DTYPE_BF16 && q->dtype != GDN_DTYPE_F16) return GDN_ERR_DTYPE;
+  if (kv0->dtype != q->dtype || kv1->dtype != q->dtype || out->dtype != q->dtype) return GDN_ERR_DTYPE;
+  if (D != 64 && D != 128 && D != 256) return GDN_ERR_HEAD_DIM;
+  if (q->stride[2] != 1 || out->stride[2] != 1 || kv0->stride[kd] != 1 || kv1->stride[kd] != 1)
+    return GDN_ERR_STRIDE;
+  if (numel(q) > 0 && (!vec_ok(q, 16) || !vec_ok(out, 16))) return GDN_ERR_ALIGN;
+  if (numel(kv0) > 0 && (!vec_ok(kv0, 16) || !vec_ok(kv1, 16))) return GDN_ERR_ALIGN;
+  return GDN_OK;
+}
+
+// paged caches (blocks, page, Hkv, D), block table (N, cols), context lengths (N,)
+int check_paged(const gdn_tensor* kc, const gdn_tensor* vc, const gdn_tensor* tab, const gdn_tensor* ctx,
+                int64_t N) {
+  GDN_TRY(check_desc(kc, 4));
+  GDN_TRY(check_desc(vc, 4));
+  GDN_TRY(check_desc(tab, 2));
+  GDN_TRY(check_desc(ctx, 1));
+  for (int i = 0; i < 4; ++i)
+    if (vc->shape[i] != kc->shape[i]) return GDN_ERR_SHAPE;
+  if (tab->shape[0] != N || ctx->shape[0] != N) return GDN_ERR_SHAPE;
+  if (kc->shape[1] <= 0 || kc->shape[1] > INT32_MAX) return GDN_ERR_SHAPE;
+  if (!is_index(tab->dtype) || !is_index(ctx->dtype)) return GDN_ERR_DTYPE;
+  if (tab->stride[1] != 1 || ctx->stride[0] != 1) return GDN_ERR_STRIDE;
+  return GDN_OK;
+}
+
 }  // namespace
 
 GDN_EXPORT int gdn_abi_version(void) { return GDN_ABI_VERSION; }
@@ -354,4 +402,76 @@ GDN_EXPORT int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_te
     return GDN_ERR_STRIDE;
   if (T * H > kMaxGrid) return GDN_ERR_RANGE;
   return launch_rc(gdn_gating_launch(a, b, A_log, dt_bias, g, beta, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                      const gdn_tensor* cu_seqlens, gdn_tensor* out, int64_t max_seqlen, float scale,
+                                      int32_t causal, void* stream) {
+  GDN_TRY(check_desc(q, 3));
+  GDN_TRY(check_desc(k, 3));
+  GDN_TRY(check_desc(v, 3));
+  GDN_TRY(check_desc(out, 3));
+  GDN_TRY(check_desc(cu_seqlens, 1));
+  if (k->shape[0] != q->shape[0] || v->shape[0] != q->shape[0] || v->shape[1] != k->shape[1]) return GDN_ERR_SHAPE;
+  if (cu_seqlens->shape[0] < 1 || max_seqlen < 0) return GDN_ERR_SHAPE;
+  GDN_TRY(check_attn_qo(q, out, k, v, k->shape[1]));
+  if (!is_index(cu_seqlens->dtype)) return GDN_ERR_DTYPE;
+  if (cu_seqlens->stride[0] != 1) return GDN_ERR_STRIDE;
+  const int64_t R = q->shape[1] / k->shape[1];
+  const int64_t gh = R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1);
+  if (cu_seqlens->shape[0] - 1 > kMaxGridYZ || q->shape[1] / gh > kMaxGridYZ || max_seqlen / 32 > kMaxGrid)
+    return GDN_ERR_RANGE;
+  return launch_rc(attn_varlen_prefill_launch(q, k, v, cu_seqlens, out, max_seqlen, scale, causal,
+                                              reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                                       const gdn_tensor* block_tables, const gdn_tensor* context_lens,
+                                       const gdn_tensor* cu_seqlens, gdn_tensor* out, int64_t max_seqlen,
+                                       float scale, void* stream) {
+  GDN_TRY(check_desc(q, 3));
+  GDN_TRY(check_desc(out, 3));
+  GDN_TRY(check_desc(cu_seqlens, 1));
+  if (cu_seqlens->shape[0] < 1 || max_seqlen < 0) return GDN_ERR_SHAPE;
+  const int64_t N = cu_seqlens->shape[0] - 1;
+  GDN_TRY(check_paged(k_cache, v_cache, block_tables, context_lens, N));
+  GDN_TRY(check_attn_qo(q, out, k_cache, v_cache, k_cache->shape[2]));
+  if (!is_index(cu_seqlens->dtype)) return GDN_ERR_DTYPE;
+  if (cu_seqlens->stride[0] != 1) return GDN_ERR_STRIDE;
+  const int64_t R = q->shape[1] / k_cache->shape[2];
+  const int64_t gh = R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1);
+  if (N > kMaxGridYZ || q->shape[1] / gh > kMaxGridYZ || max_seqlen / 32 > kMaxGrid) return GDN_ERR_RANGE;
+  return launch_rc(attn_paged_prefill_launch(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens, out,
+                                             max_seqlen, scale, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim,
+                                                         int32_t num_splits) {
+  if (num_seqs < 0 || num_q_heads < 0 || head_dim < 0 || num_splits <= 1) return 0;
+  return num_seqs * num_q_heads * (int64_t)num_splits * (head_dim + 4);
+}
+
+GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                                      const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
+                                      gdn_tensor* workspace, int32_t num_splits, float scale, void* stream) {
+  GDN_TRY(check_desc(q, 3));
+  GDN_TRY(check_desc(out, 3));
+  const int64_t B = q->shape[0];
+  GDN_TRY(check_paged(k_cache, v_cache, block_tables, context_lens, B));
+  GDN_TRY(check_attn_qo(q, out, k_cache, v_cache, k_cache->shape[2]));
+  if (num_splits < 1 || num_splits > kMaxDecodeSplits) return GDN_ERR_RANGE;
+  const int64_t Hkv = k_cache->shape[2], R = q->shape[1] / Hkv;
+  if (B > kMaxGridYZ || Hkv * ((R + 15) / 16) > kMaxGridYZ) return GDN_ERR_RANGE;
+  float* ws = nullptr;
+  if (num_splits > 1) {
+    GDN_TRY(check_desc(workspace, 1));
+    if (workspace->dtype != GDN_DTYPE_F32) return GDN_ERR_DTYPE;
+    if (workspace->stride[0] != 1) return GDN_ERR_STRIDE;
+    if (workspace->shape[0] < paged_attention_decode_workspace_size(B, q->shape[1], q->shape[2], num_splits))
+      return GDN_ERR_SHAPE;
+    if (B > 0 && !aligned(workspace, 16)) return GDN_ERR_ALIGN;
+    ws = reinterpret_cast<float*>(workspace->data);
+  }
+  return launch_rc(attn_paged_decode_launch(q, k_cache, v_cache, block_tables, context_lens, out, ws, num_splits,
+                                            scale, reinterpret_cast<hipStream_t>(stream)));
 }

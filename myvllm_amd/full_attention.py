@@ -1,0 +1,140 @@
+"""Full attention of the hybrid stack's attention layers, on HIP kernels.
+
+Same names, arguments and results as ``ops/full_attention.py`` of
+yuyifanbupt/myvllm (``flash_attention_prefill`` ``:114-173``,
+``paged_flash_attention_decode`` ``:282-335``, ``paged_flash_attention_prefill``
+``:454-512``), with the output on q's device in q's dtype.  GQA: query head h
+reads kv head ``h // (Hq // Hkv)``.  Supported: bf16 / fp16, head dim 64, 128
+or 256 for q, k and v alike.
+
+Differences from the reference kernels, all in the reference's disfavour
+(each is a defect of its Triton code, not an intended behaviour): K and V of
+sequence n are read from that sequence's rows (``:57-72`` read from token 0),
+the output's dim stride is the dim stride (``:76``), the non-causal path masks
+keys past the sequence end, and the paged prefill reads its work list and
+``cu_seqlens`` correctly (``:378-380``); a query with no visible key gives a
+zero row instead of 0/0.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_DECODE_TARGET_WAVES = 2048
+
+
+def _max_seqlen(cu_seqlens: torch.Tensor) -> int:
+    if cu_seqlens.numel() < 2:
+        return 0
+    return int((cu_seqlens[1:] - cu_seqlens[:-1]).max().item())
+
+
+def flash_attention_prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    scale: float,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    head_v_dim: int,
+    is_causal: bool,
+    max_seqlen: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Varlen attention over packed sequences: q (T, Hq, D), k, v (T, Hkv, D) ->
+    (T, Hq, D).  ``max_seqlen`` (the longest sequence) is read from
+    ``cu_seqlens`` when not given, one host sync as in the reference (``:139``)."""
+    if q.shape[1] != num_heads or k.shape[1] != num_kv_heads or q.shape[2] != head_dim or v.shape[2] != head_v_dim:
+        raise ValueError("q/k/v shapes disagree with num_heads/num_kv_heads/head_dim/head_v_dim")
+    dev = _lib.require_device(q, k, v, cu_seqlens)
+    if max_seqlen is None:
+        max_seqlen = _max_seqlen(cu_seqlens)
+    if out is None:
+        out = torch.empty(q.shape[0], q.shape[1], head_v_dim, dtype=q.dtype, device=dev)
+    D = _lib.describe
+    rc = _lib.load().flash_attention_varlen(
+        D(q), D(k), D(v), D(cu_seqlens), D(out), int(max_seqlen), float(scale), int(bool(is_causal)),
+        _lib.stream_handle(dev),
+    )
+    _lib.check("flash_attention_varlen", rc)
+    return out
+
+
+def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int) -> int:
+    """Key splits per (sequence, kv head) so that the decode launch has about
+    2048 waves (8 per CU); 1 when the batch alone fills the GPU."""
+    waves = max(1, num_seqs * num_kv_heads * ((num_q_heads // max(num_kv_heads, 1) + 15) // 16))
+    return max(1, min(256, -(-_DECODE_TARGET_WAVES // waves)))
+
+
+def paged_flash_attention_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    num_splits: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One query per sequence over its paged cache: q (B, Hq, D), caches
+    (num_blocks, block_size, Hkv, D), block_tables (B, max_blocks),
+    context_lens (B,) -> (B, Hq, D).  No host sync."""
+    if k_cache.shape[1] != block_size:
+        raise ValueError(f"block_size {block_size} != k_cache.shape[1] {k_cache.shape[1]}")
+    dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens)
+    B, Hq, Dh = q.shape
+    if num_splits is None:
+        num_splits = decode_num_splits(B, Hq, k_cache.shape[2])
+    lib = _lib.load()
+    ws = None
+    n_ws = lib.paged_attention_decode_workspace_size(B, Hq, Dh, int(num_splits))
+    if n_ws > 0:
+        ws = torch.empty(n_ws, dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty(B, Hq, v_cache.shape[-1], dtype=q.dtype, device=dev)
+    D = _lib.describe
+    rc = lib.paged_attention_decode(
+        D(q), D(k_cache), D(v_cache), D(block_tables), D(context_lens), D(out),
+        D(ws) if ws is not None else None, int(num_splits), float(scale), _lib.stream_handle(dev),
+    )
+    _lib.check("paged_attention_decode", rc)
+    return out
+
+
+def paged_flash_attention_prefill(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    block_m_indices: torch.Tensor | None,
+    scale: float,
+    page_block_size: int,
+    max_seqlen: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Prefill over a paged cache that already holds the new keys: query i of
+    sequence n sits at position ``context_lens[n] - len_n + i`` and attends
+    causally to the cached keys.  ``block_m_indices`` (the reference's
+    per-16-row work list) is accepted for interface parity and not needed:
+    the kernel tiles the queries itself from ``cu_seqlens``."""
+    if k_cache.shape[1] != page_block_size:
+        raise ValueError(f"page_block_size {page_block_size} != k_cache.shape[1] {k_cache.shape[1]}")
+    dev = _lib.require_device(q, k_cache, v_cache, page_block_tables, context_lens, cu_seqlens)
+    if max_seqlen is None:
+        max_seqlen = _max_seqlen(cu_seqlens)
+    if out is None:
+        out = torch.empty(q.shape[0], q.shape[1], v_cache.shape[-1], dtype=q.dtype, device=dev)
+    D = _lib.describe
+    rc = _lib.load().paged_attention_prefill(
+        D(q), D(k_cache), D(v_cache), D(page_block_tables), D(context_lens), D(cu_seqlens), D(out),
+        int(max_seqlen), float(scale), _lib.stream_handle(dev),
+    )
+    _lib.check("paged_attention_prefill", rc)
+    return out

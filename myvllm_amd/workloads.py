@@ -190,3 +190,90 @@ def decode_fused_case(B: int = 256, num_slots: int = 1024, seed: int = 0, Hk: in
     idx = torch.randperm(num_slots, generator=gen)[:B].to(torch.int32)
     st = torch.randn(num_slots, Hv, K, V, generator=gen) * 0.1 if state else None
     return FusedDecodeCase(x, w, cs, cidx, a, b, A_log, dt_bias, st, idx, Hk)
+
+
+# ---- full-attention layers of the hybrid stack ---------------------------------------
+# 16 query heads, 2 kv heads, head dim 256 (configs/qwen3_5.py:34, :93, :97).
+ATTN_HQ, ATTN_HKV, ATTN_D = 16, 2, 256
+
+
+@dataclass
+class AttnVarlenCase:
+    q: torch.Tensor  # (T, Hq, D)
+    k: torch.Tensor  # (T, Hkv, D)
+    v: torch.Tensor
+    cu: torch.Tensor  # (N+1,) int32
+    scale: float
+
+    @property
+    def max_len(self) -> int:
+        return int((self.cu[1:] - self.cu[:-1]).max()) if self.cu.numel() > 1 else 0
+
+
+def attn_varlen_case(lengths, seed: int = 0, Hq: int = ATTN_HQ, Hkv: int = ATTN_HKV, D: int = ATTN_D,
+                     dtype=torch.bfloat16) -> AttnVarlenCase:
+    """Packed q, k, v ~N(0, 1) in ``dtype`` for the given lengths; scale D^-1/2."""
+    gen = torch.Generator().manual_seed(seed)
+    cu = cu_from_lengths(lengths)
+    T = int(cu[-1])
+    q = torch.randn(T, Hq, D, generator=gen).to(dtype)
+    k = torch.randn(T, Hkv, D, generator=gen).to(dtype)
+    v = torch.randn(T, Hkv, D, generator=gen).to(dtype)
+    return AttnVarlenCase(q, k, v, cu, D ** -0.5)
+
+
+def attn_prefill_32k_case(seed: int = 0) -> AttnVarlenCase:
+    """Causal varlen prefill of an attention layer over the same 16 sequence
+    lengths as the GDN prefill workload (uniform in [512, 4096], seed 0)."""
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(512, 4097, (16,), generator=gen).tolist()
+    return attn_varlen_case(lengths, seed=seed + 1)
+
+
+@dataclass
+class PagedCase:
+    q: torch.Tensor  # (T, Hq, D): the new tokens (one per sequence for decode)
+    k_cache: torch.Tensor  # (num_blocks, page, Hkv, D)
+    v_cache: torch.Tensor
+    block_tables: torch.Tensor  # (N, max_blocks) int32, unused entries -1
+    context_lens: torch.Tensor  # (N,) int32
+    cu: torch.Tensor  # (N+1,) int32 rows of q per sequence
+    scale: float
+    page: int
+
+    @property
+    def max_len(self) -> int:
+        return int((self.cu[1:] - self.cu[:-1]).max()) if self.cu.numel() > 1 else 0
+
+
+def paged_case(context_lens, new_lens, page: int = 16, seed: int = 0, Hq: int = ATTN_HQ, Hkv: int = ATTN_HKV,
+               D: int = ATTN_D, dtype=torch.bfloat16, spare_blocks: int = 3) -> PagedCase:
+    """A paged KV cache holding ``context_lens[n]`` keys of sequence n (the
+    last ``new_lens[n]`` of which are the new tokens' own keys), pages drawn
+    as a random permutation of the cache blocks; q ~N(0, 1) for the new tokens."""
+    gen = torch.Generator().manual_seed(seed)
+    ctx = torch.as_tensor(context_lens, dtype=torch.int64)
+    new = torch.as_tensor(new_lens, dtype=torch.int64)
+    npages = (ctx + page - 1) // page
+    num_blocks = int(npages.sum()) + spare_blocks
+    cols = max(int(npages.max()) if len(npages) else 1, 1)
+    kc = torch.randn(num_blocks, page, Hkv, D, generator=gen).to(dtype)
+    vc = torch.randn(num_blocks, page, Hkv, D, generator=gen).to(dtype)
+    perm = torch.randperm(num_blocks, generator=gen)
+    tab = torch.full((len(ctx), cols), -1, dtype=torch.int32)
+    o = 0
+    for n, p in enumerate(npages.tolist()):
+        tab[n, :p] = perm[o:o + p].to(torch.int32)
+        o += p
+    cu = cu_from_lengths(new.tolist())
+    q = torch.randn(int(cu[-1]), Hq, D, generator=gen).to(dtype)
+    return PagedCase(q, kc, vc, tab, ctx.to(torch.int32), cu, D ** -0.5, page)
+
+
+def attn_decode_case(B: int = 256, seed: int = 0, page: int = 16, lo: int = 512, hi: int = 4096,
+                     **kw) -> PagedCase:
+    """Paged decode of an attention layer: B sequences with context lengths
+    uniform in [lo, hi], one new query each, 16-token pages."""
+    gen = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (B,), generator=gen).tolist()
+    return paged_case(ctx, [1] * B, page=page, seed=seed + 1, **kw)

@@ -19,7 +19,7 @@ defects -- K/V read from token 0 of the batch instead of the sequence start
   masked score -1e10 and running max start -1e10 (``:93``, ``:97``) give the
   softmax of the unmasked keys.
 
-Computed here in fp64 without the rounding of P.
+Computed here in fp64 without the rounding of P; results are returned in fp64.
 """
 from __future__ import annotations
 
@@ -50,7 +50,18 @@ def flash_attention_prefill_ref(q, k, v, cu_seqlens, scale, is_causal=True):
         s, e = cu[n], cu[n + 1]
         if e > s:
             o[s:e] = _attend(q[s:e].double(), k[s:e].double(), v[s:e].double(), scale, torch.arange(e - s), is_causal)
-    return o.to(q.dtype)
+    return o
+
+
+def attention_rows_ref(q_rows, k_seq, v_seq, pos, scale, causal=True):
+    """Selected queries of one sequence: q_rows (n, Hq, D) at positions
+    ``pos`` over the sequence's keys k_seq, v_seq (m, Hkv, D), fp64."""
+    return _attend(q_rows.double(), k_seq.double(), v_seq.double(), scale, torch.as_tensor(pos), causal)
+
+
+def gather_paged(cache, table_row, L):
+    """Keys 0..L-1 of one sequence from a (blocks, page, Hkv, D) cache."""
+    return _gather(cache, table_row, L, cache.shape[1])
 
 
 def _gather(cache, table_row, L, bs):
@@ -74,7 +85,7 @@ def paged_attention_ref(q, k_cache, v_cache, block_tables, context_lens, cu_seql
         v = _gather(v_cache, block_tables[n], L, bs).double()
         pos = L - (e - s) + torch.arange(e - s)
         o[s:e] = _attend(q[s:e].double(), k, v, scale, pos, True)
-    return o.to(q.dtype)
+    return o
 
 
 def attention_loop_ref(q, k, v, scale, pos, causal):

@@ -23,7 +23,7 @@ ERR = {"NULL": -1, "NDIM": -2, "SHAPE": -3, "DTYPE": -4, "STRIDE": -5, "HEADS": 
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|char\s*\*|size_t|void)\s*\*?\s*(\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int64_t|int|char\s*\*|size_t|void)\s*\*?\s*(\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_ffi_surface():
@@ -232,3 +232,102 @@ def test_ops_reject_cpu_tensors():
     c = _conv_args()
     with pytest.raises(ValueError):
         causal_conv1d_update(c["x"][:2], c["w"], c["st"], c["idx"])
+
+
+# ---- full attention ------------------------------------------------------------------
+
+def _varlen_attn_args(T=8, Hq=4, Hkv=2, Dh=128, dtype=torch.bfloat16):
+    return dict(q=torch.zeros(T, Hq, Dh, dtype=dtype), k=torch.zeros(T, Hkv, Dh, dtype=dtype),
+                v=torch.zeros(T, Hkv, Dh, dtype=dtype), cu=torch.tensor([0, 3, T], dtype=torch.int32),
+                out=torch.zeros(T, Hq, Dh, dtype=dtype), max_len=5)
+
+
+def _call_varlen_attn(a):
+    return _lib.load().flash_attention_varlen(D(a["q"]), D(a["k"]), D(a["v"]), D(a["cu"]), D(a["out"]),
+                                              a["max_len"], 1.0, 1, None)
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "mutate, code",
+    [
+        (lambda a: a.update(q=torch.zeros(8, 4, 128, 1, dtype=torch.bfloat16)), "NDIM"),
+        (lambda a: a.update(k=torch.zeros(7, 2, 128, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(v=torch.zeros(8, 1, 128, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(out=torch.zeros(8, 4, 64, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(max_len=-1), "SHAPE"),
+        (lambda a: a.update(q=torch.zeros(8, 3, 128, dtype=torch.bfloat16), out=torch.zeros(8, 3, 128, dtype=torch.bfloat16)), "HEADS"),
+        (lambda a: a.update(q=torch.zeros(8, 4, 128), out=torch.zeros(8, 4, 128)), "DTYPE"),
+        (lambda a: a.update(v=torch.zeros(8, 2, 128, dtype=torch.float16)), "DTYPE"),
+        (lambda a: a.update(cu=torch.tensor([0.0, 8.0])), "DTYPE"),
+        (lambda a: a.update(q=torch.zeros(8, 4, 96, dtype=torch.bfloat16), k=torch.zeros(8, 2, 96, dtype=torch.bfloat16),
+                            v=torch.zeros(8, 2, 96, dtype=torch.bfloat16), out=torch.zeros(8, 4, 96, dtype=torch.bfloat16)), "HEAD_DIM"),
+        (lambda a: a.update(k=torch.zeros(8, 128, 2, dtype=torch.bfloat16).transpose(1, 2)), "STRIDE"),
+        (lambda a: a.update(q=torch.zeros(8 * 4 * 128 + 1, dtype=torch.bfloat16)[1:].view(8, 4, 128)), "ALIGN"),
+    ],
+)
+def test_varlen_attention_validation(mutate, code):
+    a = _varlen_attn_args()
+    mutate(a)
+    assert _call_varlen_attn(a) == ERR[code]
+
+
+def _paged_attn_args(B=2, Hq=4, Hkv=2, Dh=128, blocks=5, page=16, cols=3, dtype=torch.bfloat16):
+    return dict(q=torch.zeros(B, Hq, Dh, dtype=dtype), kc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype),
+                vc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype), tab=torch.zeros(B, cols, dtype=torch.int32),
+                ctx=torch.ones(B, dtype=torch.int32), out=torch.zeros(B, Hq, Dh, dtype=dtype),
+                ws=torch.zeros(B * Hq * 4 * (Dh + 4)), splits=4)
+
+
+def _call_paged_decode(a):
+    return _lib.load().paged_attention_decode(D(a["q"]), D(a["kc"]), D(a["vc"]), D(a["tab"]), D(a["ctx"]),
+                                              D(a["out"]), D(a["ws"]) if a["ws"] is not None else None,
+                                              a["splits"], 1.0, None)
+
+
+@cpu_only
+@pytest.mark.parametrize(
+    "mutate, code",
+    [
+        (lambda a: a.update(kc=torch.zeros(5, 16, 256, dtype=torch.bfloat16)), "NDIM"),
+        (lambda a: a.update(vc=torch.zeros(4, 16, 2, 128, dtype=torch.bfloat16)), "SHAPE"),
+        (lambda a: a.update(tab=torch.zeros(3, 3, dtype=torch.int32)), "SHAPE"),
+        (lambda a: a.update(ctx=torch.zeros(3, dtype=torch.int32)), "SHAPE"),
+        (lambda a: a.update(ws=torch.zeros(10)), "SHAPE"),
+        (lambda a: a.update(ws=None), "NULL"),
+        (lambda a: a.update(ws=torch.zeros(2 * 4 * 4 * 132, dtype=torch.float16)), "DTYPE"),
+        (lambda a: a.update(tab=torch.zeros(2, 3)), "DTYPE"),
+        (lambda a: a.update(tab=torch.zeros(3, 2, dtype=torch.int32).t()), "STRIDE"),
+        (lambda a: a.update(splits=0), "RANGE"),
+        (lambda a: a.update(splits=257), "RANGE"),
+        (lambda a: a.update(ws=torch.zeros(2 * 4 * 4 * 132 + 1)[1:]), "ALIGN"),
+    ],
+)
+def test_paged_decode_validation(mutate, code):
+    a = _paged_attn_args()
+    mutate(a)
+    assert _call_paged_decode(a) == ERR[code]
+
+
+@cpu_only
+def test_paged_prefill_validation():
+    a = _paged_attn_args()
+    q = torch.zeros(5, 4, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 2, 5], dtype=torch.int32)
+
+    def call(q=q, cu=cu, out=None, tab=a["tab"], ctx=a["ctx"], max_len=3):
+        out = torch.zeros_like(q) if out is None else out
+        return _lib.load().paged_attention_prefill(D(q), D(a["kc"]), D(a["vc"]), D(tab), D(ctx), D(cu), D(out),
+                                                   max_len, 1.0, None)
+
+    assert call(cu=torch.tensor([0, 5], dtype=torch.int32)) == ERR["SHAPE"]  # one sequence, two table rows
+    assert call(out=torch.zeros(5, 4, 256, dtype=torch.bfloat16)) == ERR["SHAPE"]
+    assert call(max_len=-1) == ERR["SHAPE"]
+    assert call(ctx=torch.ones(2)) == ERR["DTYPE"]
+    assert call(cu=torch.tensor([0.0, 2.0, 5.0])) == ERR["DTYPE"]
+
+
+def test_decode_workspace_size():
+    lib = _lib.load()
+    assert lib.paged_attention_decode_workspace_size(3, 16, 256, 1) == 0
+    assert lib.paged_attention_decode_workspace_size(3, 16, 256, 4) == 3 * 16 * 4 * 260
