@@ -353,6 +353,104 @@ def bench_layer(dev, steps, warmup, cpu_budget):
                          "kernel": "whole layer (GEMMs + GDN prefill FLOPs over the step time)"}}
 
 
+def bench_attn_prefill(dev, steps, warmup, cpu_budget):
+    """Causal varlen attention prefill of the hybrid stack's attention layers
+    (Hq 16, Hkv 2, D 256) over the GDN prefill workload's 16 sequence lengths."""
+    from myvllm_amd import flash_attention_prefill
+    from myvllm_amd.workloads import ATTN_D, ATTN_HKV, ATTN_HQ, attn_prefill_32k_case
+
+    case = attn_prefill_32k_case()
+    q, k, v, cu = (t.to(dev) for t in (case.q, case.k, case.v, case.cu))
+    out = torch.empty_like(q)
+    max_len = case.max_len
+
+    def step(_):
+        flash_attention_prefill(q, k, v, cu, case.scale, ATTN_HQ, ATTN_HKV, ATTN_D, ATTN_D, True,
+                                max_seqlen=max_len, out=out)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    lens = (case.cu[1:] - case.cu[:-1]).tolist()
+    tokens = int(case.cu[-1])
+    pairs = sum(n * (n + 1) // 2 for n in lens)  # (query, visible key) pairs
+    flops = 4 * ATTN_D * ATTN_HQ * pairs  # QK^T and PV, 2 FLOPs per MAC
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "tokens": tokens,
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms,
+        "tokens_per_s": tokens / (kern_ms * 1e-3),
+        "TFLOP_per_s": tflops,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_MFMA_TFLOPS, "traffic": _traffic("attn_prefill_kernel"),
+                     "flops_per_launch": flops, "kernel": "attn_prefill_kernel"},
+    }
+    if cpu_budget > 0:
+        from oracle.attention import attention_rows_ref
+
+        torch.set_num_threads(_cpu_threads())
+        n0 = lens[2]  # bounded sample: the third sequence (1,405 tokens) in full
+        s0 = int(case.cu[2])
+        sl = slice(s0, s0 + n0)
+        sec = _time_cpu(lambda: attention_rows_ref(case.q[sl], case.k[sl], case.v[sl], torch.arange(n0), case.scale),
+                        cpu_budget, max_reps=3)
+        res["cpu_baseline"] = {"value": n0 / sec, "unit": "tokens/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"one sequence of {n0} tokens, fp64 causal attention"}
+    return res
+
+
+def bench_attn_decode(dev, steps, warmup, cpu_budget):
+    """Paged decode of the attention layers: batch 256, contexts uniform in
+    [512, 4096] (602,903 cached keys), 16-token pages, Hq 16, Hkv 2, D 256."""
+    from myvllm_amd import paged_flash_attention_decode
+    from myvllm_amd.full_attention import decode_num_splits
+    from myvllm_amd.workloads import ATTN_D, ATTN_HKV, ATTN_HQ, attn_decode_case
+
+    case = attn_decode_case()
+    q, kc, vc, tab, ctx = (t.to(dev) for t in (case.q, case.k_cache, case.v_cache, case.block_tables,
+                                                case.context_lens))
+    out = torch.empty_like(q)
+    B = q.shape[0]
+    splits = decode_num_splits(B, ATTN_HQ, ATTN_HKV)
+
+    def step(_):
+        paged_flash_attention_decode(q, kc, vc, tab, ctx, case.scale, case.page, num_splits=splits, out=out)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    keys = int(case.context_lens.sum())
+    pages = int(((case.context_lens + case.page - 1) // case.page).sum())
+    # K and V rows of every cached key, q and o, the table entries and lengths
+    nbytes = keys * ATTN_HKV * ATTN_D * 2 * 2 + 2 * B * ATTN_HQ * ATTN_D * 2 + pages * 4 + B * 4
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "batch": B,
+        "cached_keys": keys,
+        "splits": splits,
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms,
+        "GB_per_s": gbs,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": _traffic("attn_decode_kernel"), "bytes_per_launch": nbytes,
+                     "kernel": "attn_decode_kernel + attn_decode_combine_kernel"},
+    }
+    if cpu_budget > 0:
+        from oracle.attention import attention_rows_ref, gather_paged
+
+        torch.set_num_threads(_cpu_threads())
+        sub = 16  # bounded sample: 16 of the 256 sequences
+
+        def cpu():
+            for b in range(sub):
+                L = int(case.context_lens[b])
+                attention_rows_ref(case.q[b:b + 1], gather_paged(case.k_cache, case.block_tables[b], L),
+                                   gather_paged(case.v_cache, case.block_tables[b], L), [L - 1], case.scale)
+
+        sec = _time_cpu(cpu, cpu_budget, max_reps=3)
+        sub_bytes = int(case.context_lens[:sub].sum()) * ATTN_HKV * ATTN_D * 2 * 2
+        res["cpu_baseline"] = {"value": sub_bytes / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"{sub} of {B} sequences, fp64 attention over gathered pages"}
+    return res
+
+
 def bench_hbm_copy(dev, steps, warmup, cpu_budget):
     """Plain 1 GiB device-to-device copy: the calibration point of the HBM
     byte counters and the copy bandwidth this device reaches."""
@@ -379,7 +477,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="all",
                     help="all, or a comma-separated list of prefill, decode, conv, conv_update, decode_fused, "
-                         "layer, hbm_copy")
+                         "layer, attn_prefill, attn_decode, hbm_copy")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     args = ap.parse_args()
@@ -394,7 +492,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "hbm_copy"}
+    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill", "attn_decode",
+             "hbm_copy"}
     chosen = set(args.workload.split(","))
     if not chosen <= (known | {"all"}):
         print(f"unknown workload(s): {sorted(chosen - known - {'all'})}", file=sys.stderr)
@@ -424,6 +523,14 @@ def main():
               f"({parts['layer']['tokens_per_s'] / 1e6:.2f} M tokens/s); stages (us): "
               + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in parts["layer"]["stages_ms"].items()),
               file=sys.stderr, flush=True)
+    if want("attn_prefill"):
+        parts["attn_prefill"] = bench_attn_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# attn_prefill: {parts['attn_prefill']['kernel_ms'] * 1e3:.1f} us/launch "
+              f"({parts['attn_prefill']['TFLOP_per_s']:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+    if want("attn_decode"):
+        parts["attn_decode"] = bench_attn_decode(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# attn_decode: {parts['attn_decode']['kernel_ms'] * 1e3:.1f} us/step "
+              f"({parts['attn_decode']['GB_per_s']:.0f} GB/s)", file=sys.stderr, flush=True)
     if "hbm_copy" in chosen:
         parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
 
@@ -444,6 +551,14 @@ def main():
         metric, value, unit = "GDN layer tokens/s", head["tokens_per_s"], "tokens/s"
         workload = ("GatedDeltaNet layer: hidden 2048, Hk 16 / Hv 32, d 128, conv 4; 4 x 2048 prefill + 128 decode "
                     "tokens in one call, bf16 weights ~N(0, 0.02), fp32 states")
+    elif head_name == "attn_prefill":
+        metric, value, unit = "attention prefill tokens/s", head["tokens_per_s"], "tokens/s"
+        workload = (f"flash_attention_varlen: causal, 16 varlen seqs (lengths U[512,4096], seed 0), "
+                    f"{head['tokens']} tokens, Hq 16 / Hkv 2, d 256, bf16")
+    elif head_name == "attn_decode":
+        metric, value, unit = "attention paged decode HBM GB/s", head["GB_per_s"], "GB/s"
+        workload = ("paged_attention_decode: batch 256, contexts U[512,4096] (602,903 keys), 16-token pages, "
+                    "Hq 16 / Hkv 2, d 256, bf16")
     elif head_name == "hbm_copy":
         metric, value, unit = "device copy HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "hbm_copy: 1 GiB device-to-device copy (read + write counted)"
