@@ -410,7 +410,7 @@ def bench_attn_decode(dev, steps, warmup, cpu_budget):
                                                 case.context_lens))
     out = torch.empty_like(q)
     B = q.shape[0]
-    splits = decode_num_splits(B, ATTN_HQ, ATTN_HKV)
+    splits = decode_num_splits(B, ATTN_HQ, ATTN_HKV, case.block_tables.shape[1] * case.page)
 
     def step(_):
         paged_flash_attention_decode(q, kc, vc, tab, ctx, case.scale, case.page, num_splits=splits, out=out)

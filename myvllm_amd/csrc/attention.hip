@@ -295,9 +295,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 // heads, key split).  The query heads of one kv head are the 16 columns of
 // S^T = K Q^T (16x16x32 MFMA, K fragments straight from global memory), the
 // V tile goes through a wave-private LDS tile for the transposed read of
-// O^T = V^T P^T (16x16x16 MFMA).  With more than one split the wave writes
-// its unnormalised O, running maximum and row sum to the workspace and
-// attn_decode_combine_kernel merges the splits.
+// O^T = V^T P^T (16x16x16 MFMA).  Split s covers keys [s chunk, (s+1) chunk)
+// of the table's capacity (chunk fixed per launch), so the waves of all
+// sequences get equal work and splits past a sequence's length exit at once.
+// With more than one split the wave writes its unnormalised O, running
+// maximum and row sum to the workspace and attn_decode_combine_kernel merges
+// the splits that hold keys.  With a page size that is a multiple of 16 a
+// 16-key tile lies in one page: its block id is one wave-uniform load, issued
+// a tile ahead of the K/V loads that use it.
 struct DecodeArgs {
   const void* q;
   int64_t q_ss, q_sh;
@@ -307,12 +312,13 @@ struct DecodeArgs {
   const void* ctx;
   PagedTable tab;
   float* part;  // (B, Hq, splits, D + 4): O, m, l (rows padded to 16 bytes)
+  int64_t chunk;  // keys per split, a multiple of 16
   int32_t B, Hq, Hkv, splits;
   float c;
   bool ctx64;
 };
 
-template <typename T, int D>
+template <typename T, int D, bool PAGE16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_decode_kernel(const DecodeArgs a) {
   typedef Mma<T> M;
   typedef typename M::v8 v8;
@@ -327,19 +333,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
   const int lane = threadIdx.x;
   const int split = blockIdx.x;
   const int64_t b = blockIdx.z;
+  const int64_t ctx = load_index(a.ctx, b, a.ctx64);
+  const int64_t L = clamp64(ctx, 0, a.tab.cols * a.tab.page);
+  const int64_t k_lo = a.chunk * split;
+  if (split > 0 && k_lo >= L) return;  // no keys: the combine skips this split
+  const int64_t k_hi = k_lo + a.chunk < L ? k_lo + a.chunk : L;
+  const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
+
   const int R = a.Hq / a.Hkv, hgroups = (R + 15) / 16;
   const int kvh = blockIdx.y / hgroups;
   const int hcol = (blockIdx.y % hgroups) * 16 + (lane & 15);
   const bool hvalid = hcol < R;
   const int head = kvh * R + (hvalid ? hcol : 0);
   const int grp = lane >> 4;
-
-  const int64_t ctx = load_index(a.ctx, b, a.ctx64);
-  const int64_t L = clamp64(ctx, 0, a.tab.cols * a.tab.page);
-  const int64_t chunk = ((L + a.splits - 1) / a.splits + 15) / 16 * 16;
-  const int64_t k_lo = chunk * split;
-  const int64_t k_hi = k_lo + chunk < L ? k_lo + chunk : L;
-  const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
 
   v8 qf[NKS];
   {
@@ -348,13 +354,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     for (int s = 0; s < NKS; ++s) qf[s] = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
   }
 
+  // block id of tile t's page (PAGE16), -1 past the range or for an entry
+  // outside [0, num_blocks)
+  auto tile_block = [&](int t) -> int64_t {
+    if (t >= ntiles) return -1;
+    const int64_t col = (k_lo + 16 * (int64_t)t) / a.tab.page;
+    const int64_t blk = load_index(a.tab.table, b * a.tab.row_stride + col, a.tab.is64);
+    return blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
+  };
+  // row r of tile t
+  auto row_ptr = [&](const KvSource& src, int t, int64_t blk, int r) -> const char* {
+    const int64_t j = k_lo + 16 * (int64_t)t + r;
+    if (j >= k_hi) return nullptr;
+    if (PAGE16) {
+      if (blk < 0) return nullptr;
+      return src.base + blk * src.sb + (j % a.tab.page) * src.st + kvh * src.sh;
+    }
+    return kv_row<true>(src, a.tab, b, 0, j, kvh);
+  };
+
   v8 kf[NKS];
   uint4 vr[NLD];
-  auto load_tile = [&](int t, v8* kd) {
-    const int64_t j0 = k_lo + 16 * (int64_t)t;
+  auto load_tile = [&](int t, int64_t blk, v8* kd) {
     {
-      const int64_t j = j0 + (lane & 15);
-      const char* pk = j < k_hi ? kv_row<true>(a.k, a.tab, b, 0, j, kvh) : nullptr;
+      const char* pk = row_ptr(a.k, t, blk, lane & 15);
 #pragma unroll
       for (int s = 0; s < NKS; ++s)
         kd[s] = pk ? *reinterpret_cast<const v8*>(pk + 2 * (32 * s + 8 * grp)) : v8{};
@@ -362,8 +385,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-      const int64_t j = j0 + row;
-      const char* pv = j < k_hi ? kv_row<true>(a.v, a.tab, b, 0, j, kvh) : nullptr;
+      const char* pv = row_ptr(a.v, t, blk, row);
       vr[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
     }
   };
@@ -374,7 +396,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
   float m_used = -INFINITY, lsum = 0.f;
   const float c = a.c;
 
-  if (ntiles > 0) load_tile(0, kf);
+  int64_t blk_next = PAGE16 ? tile_block(1) : -1;
+  if (ntiles > 0) load_tile(0, PAGE16 ? tile_block(0) : -1, kf);
   for (int t = 0; t < ntiles; ++t) {
     // V tile t to LDS (the previous tile's transposed reads were issued
     // earlier by this wave, and LDS operations of a wave complete in order)
@@ -386,7 +409,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     f32x4 s = f32x4{};
 #pragma unroll
     for (int k = 0; k < NKS; ++k) s = M::m16k32(kf[k], qf[k], s);
-    if (t + 1 < ntiles) load_tile(t + 1, kf);
+    if (t + 1 < ntiles) load_tile(t + 1, blk_next, kf);
+    if (PAGE16) blk_next = tile_block(t + 2);
 
     // scores: lane holds head column lane % 16, keys 4 grp + r of the tile
     const int64_t j0 = k_lo + 16 * (int64_t)t;
@@ -463,12 +487,15 @@ __global__ __launch_bounds__(64) void attn_decode_combine_kernel(const DecodeArg
   const int head = (int)(bh % a.Hq);
   constexpr int PS = D + 4;
   const float* pp = a.part + bh * a.splits * (int64_t)PS;
+  const int64_t L = clamp64(load_index(a.ctx, b, a.ctx64), 0, a.tab.cols * a.tab.page);
+  int64_t nsp = (L + a.chunk - 1) / a.chunk;
+  const int nsplit = (int)(nsp < 1 ? 1 : (nsp > a.splits ? a.splits : nsp));
   float mx = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) mx = fmaxf(mx, pp[s * PS + D]);
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, pp[s * PS + D]);
   constexpr int E = D / 64;
   float acc[E] = {};
   float l = 0.f;
-  for (int s = 0; s < a.splits; ++s) {
+  for (int s = 0; s < nsplit; ++s) {
     const float ms = pp[s * PS + D];
     if (ms == -INFINITY) continue;
     const float wgt = exp2_fast(ms - mx);
@@ -538,7 +565,10 @@ template <typename T, int D>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t st) {
   const int hgroups = (a.Hq / a.Hkv + 15) / 16;
   const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv * hgroups), (unsigned)a.B);
-  hipLaunchKernelGGL((attn_decode_kernel<T, D>), grid, dim3(64), 0, st, a);
+  if (a.tab.page % 16 == 0)
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, true>), grid, dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, false>), grid, dim3(64), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)((int64_t)a.B * a.Hq)), dim3(64), 0, st, a);
@@ -622,6 +652,11 @@ hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, c
   a.Hkv = (int32_t)kc->shape[2];
   a.splits = splits;
   a.c = scale * kLog2e;
+  {
+    const int64_t cap = a.tab.cols * (int64_t)a.tab.page;
+    const int64_t per = (cap + splits - 1) / splits;
+    a.chunk = per < 16 ? 16 : (per + 15) / 16 * 16;
+  }
   const int D = (int)q->shape[2];
   if (q->dtype == GDN_DTYPE_BF16) {
     if (D == 64) return launch_decode_t<bf16_t, 64>(a, st);

@@ -21,7 +21,8 @@ import torch
 
 from . import _lib
 
-_DECODE_TARGET_WAVES = 2048
+_DECODE_SPLIT_KEYS = 256
+_DECODE_MAX_SPLITS = 256
 
 
 def _max_seqlen(cu_seqlens: torch.Tensor) -> int:
@@ -63,11 +64,17 @@ def flash_attention_prefill(
     return out
 
 
-def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int) -> int:
-    """Key splits per (sequence, kv head) so that the decode launch has about
-    2048 waves (8 per CU); 1 when the batch alone fills the GPU."""
-    waves = max(1, num_seqs * num_kv_heads * ((num_q_heads // max(num_kv_heads, 1) + 15) // 16))
-    return max(1, min(256, -(-_DECODE_TARGET_WAVES // waves)))
+def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int, capacity: int) -> int:
+    """Key splits of the decode launch.  Split s covers keys [s c, (s+1) c) of
+    the block table's ``capacity`` (max_blocks x page) with c = capacity /
+    splits, and splits past a sequence's length exit at once, so the splits
+    are what balances sequences of different lengths: about 256 keys per
+    split, fewer splits once the batch gives 16 split-rows of waves on its own
+    (more keys per wave, less partial-result traffic), at most 256."""
+    rows = max(1, num_seqs * num_kv_heads * ((num_q_heads // max(num_kv_heads, 1) + 15) // 16))
+    by_keys = -(-max(capacity, 1) // _DECODE_SPLIT_KEYS)
+    by_waves = max(16, -(-8192 // rows))
+    return max(1, min(_DECODE_MAX_SPLITS, by_keys, by_waves))
 
 
 def paged_flash_attention_decode(
@@ -89,7 +96,7 @@ def paged_flash_attention_decode(
     dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens)
     B, Hq, Dh = q.shape
     if num_splits is None:
-        num_splits = decode_num_splits(B, Hq, k_cache.shape[2])
+        num_splits = decode_num_splits(B, Hq, k_cache.shape[2], block_tables.shape[1] * block_size)
     lib = _lib.load()
     ws = None
     n_ws = lib.paged_attention_decode_workspace_size(B, Hq, Dh, int(num_splits))
