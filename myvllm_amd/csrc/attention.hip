@@ -53,6 +53,15 @@ GDN_DEVICE float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 GDN_DEVICE int64_t clamp64(int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); }
 
+// An index at a wave-uniform position read through the scalar data cache (a
+// constant-address-space load): its wait is on the scalar/LDS counter, so it
+// does not drain the vector loads in flight.  Only for read-only inputs.
+typedef const int32_t __attribute__((address_space(4))) * const_i32_ptr;
+typedef const int64_t __attribute__((address_space(4))) * const_i64_ptr;
+GDN_DEVICE int64_t load_index_scalar(const void* p, int64_t i, bool is64) {
+  return is64 ? __builtin_bit_cast(const_i64_ptr, p)[i] : (int64_t)__builtin_bit_cast(const_i32_ptr, p)[i];
+}
+
 // Row j of a key or value source: packed varlen rows (row s0 + j) or paged
 // rows (block table[n][j / page], slot j % page).  nullptr past the valid
 // range or for a table entry outside [0, num_blocks): such rows read as zero.
@@ -302,7 +311,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 // maximum and row sum to the workspace and attn_decode_combine_kernel merges
 // the splits that hold keys.  With a page size that is a multiple of 16 a
 // 16-key tile lies in one page: its block id is one wave-uniform load, issued
-// a tile ahead of the K/V loads that use it.
+// a tile ahead of the K/V loads that use it.  The kvw kv heads of a workgroup
+// (one wave each) read the interleaved head rows of the same cache slots at
+// about the same time, so each page is streamed as one contiguous region.
 struct DecodeArgs {
   const void* q;
   int64_t q_ss, q_sh;
@@ -313,13 +324,18 @@ struct DecodeArgs {
   PagedTable tab;
   float* part;  // (B, Hq, splits, D + 4): O, m, l (rows padded to 16 bytes)
   int64_t chunk;  // keys per split, a multiple of 16
-  int32_t B, Hq, Hkv, splits;
+  int32_t B, Hq, Hkv, splits, kvw;
   float c;
   bool ctx64;
 };
 
+// LDS bytes of one decode wave: a 16-row V tile with a 32-byte row skew and
+// the wave's query fragments
+template <typename T, int D>
+constexpr size_t decode_lds_per_wave() { return (size_t)16 * (D + 16) * sizeof(T) + (size_t)(D / 32) * 64 * 16; }
+
 template <typename T, int D, bool PAGE16>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void attn_decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_decode_kernel(const DecodeArgs a) {
   typedef Mma<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -328,9 +344,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
   constexpr int NDT = D / 16;
   constexpr int CH = D / 8;
   constexpr int NLD = 16 * CH / 64;
-  __shared__ __align__(16) T vs[16 * LDV];
-
-  const int lane = threadIdx.x;
+  extern __shared__ __align__(16) char decode_smem[];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // this wave's LDS: the V tile, then its query fragments
+  T* vs = reinterpret_cast<T*>(decode_smem + wv * decode_lds_per_wave<T, D>());
+  v8* qs = reinterpret_cast<v8*>(vs + 16 * LDV);
   const int split = blockIdx.x;
   const int64_t b = blockIdx.z;
   const int64_t ctx = load_index(a.ctx, b, a.ctx64);
@@ -341,25 +359,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
   const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
 
   const int R = a.Hq / a.Hkv, hgroups = (R + 15) / 16;
-  const int kvh = blockIdx.y / hgroups;
+  const int kvh = (blockIdx.y / hgroups) * a.kvw + wv;
   const int hcol = (blockIdx.y % hgroups) * 16 + (lane & 15);
   const bool hvalid = hcol < R;
   const int head = kvh * R + (hvalid ? hcol : 0);
   const int grp = lane >> 4;
 
-  v8 qf[NKS];
+  // query fragments (B operand of S^T): lane holds head column lane % 16,
+  // dims 32 s + 8 grp .. +7; kept in LDS to leave registers for two tiles in flight
   {
     const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_ss + (int64_t)head * a.q_sh + 8 * grp;
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) qf[s] = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
+    for (int s = 0; s < NKS; ++s) qs[s * 64 + lane] = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
   }
 
   // block id of tile t's page (PAGE16), -1 past the range or for an entry
   // outside [0, num_blocks)
   auto tile_block = [&](int t) -> int64_t {
-    if (t >= ntiles) return -1;
+    if (!PAGE16 || t >= ntiles) return -1;
     const int64_t col = (k_lo + 16 * (int64_t)t) / a.tab.page;
-    const int64_t blk = load_index(a.tab.table, b * a.tab.row_stride + col, a.tab.is64);
+    const int64_t blk = load_index_scalar(a.tab.table, b * a.tab.row_stride + col, a.tab.is64);
     return blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
   };
   // row r of tile t
@@ -372,21 +391,44 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     }
     return kv_row<true>(src, a.tab, b, 0, j, kvh);
   };
-
-  v8 kf[NKS];
-  uint4 vr[NLD];
-  auto load_tile = [&](int t, int64_t blk, v8* kd) {
+  auto load_tile = [&](int t, int64_t blk, uint4* kd, uint4* vd) {
+    if (PAGE16) {
+      // one page per tile: buffer loads through a descriptor of this kv
+      // head's rows of the page (32-bit offsets, rows past the range read 0)
+      const int64_t j0 = k_lo + 16 * (int64_t)t;
+      const int64_t nv = t < ntiles ? k_hi - j0 : 0;
+      const uint32_t nvalid = blk < 0 ? 0u : (uint32_t)(nv < 16 ? nv : 16);
+      const uint32_t r0 = (uint32_t)(j0 % a.tab.page);
+      const int64_t bb = blk < 0 ? 0 : blk;
+      const uint32_t bytes = blk < 0 ? 0u : (uint32_t)(a.tab.page * a.k.st);
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(a.k.base + bb * a.k.sb + kvh * a.k.sh), 0, bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(a.v.base + bb * a.v.sb + kvh * a.v.sh), 0, bytes, 0x00020000);
+      const uint32_t kr = (uint32_t)(lane & 15);
+      const uint32_t ko = kr < nvalid ? (r0 + kr) * (uint32_t)a.k.st + 16u * grp : 0x80000000u;
+#pragma unroll
+      for (int s = 0; s < NKS; ++s)
+        kd[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64u * s, 0, 0));
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const uint32_t cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+        const uint32_t vo = row < nvalid ? (r0 + row) * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+      }
+      return;
+    }
     {
       const char* pk = row_ptr(a.k, t, blk, lane & 15);
 #pragma unroll
       for (int s = 0; s < NKS; ++s)
-        kd[s] = pk ? *reinterpret_cast<const v8*>(pk + 2 * (32 * s + 8 * grp)) : v8{};
+        kd[s] = pk ? *reinterpret_cast<const uint4*>(pk + 2 * (32 * s + 8 * grp)) : uint4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
       const char* pv = row_ptr(a.v, t, blk, row);
-      vr[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+      vd[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
     }
   };
 
@@ -396,23 +438,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
   float m_used = -INFINITY, lsum = 0.f;
   const float c = a.c;
 
-  int64_t blk_next = PAGE16 ? tile_block(1) : -1;
-  if (ntiles > 0) load_tile(0, PAGE16 ? tile_block(0) : -1, kf);
-  for (int t = 0; t < ntiles; ++t) {
-    // V tile t to LDS (the previous tile's transposed reads were issued
-    // earlier by this wave, and LDS operations of a wave complete in order)
+  // first half of a tile: its V rows to LDS (the previous tile's transposed
+  // reads were issued earlier by this wave, and LDS operations of a wave
+  // complete in order) and its scores; the tile's registers are free after it
+  auto scores = [&](const uint4* kd, const uint4* vd) -> f32x4 {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-      *reinterpret_cast<uint4*>(&vs[row * LDV + 8 * ch]) = vr[i];
+      *reinterpret_cast<uint4*>(&vs[row * LDV + 8 * ch]) = vd[i];
     }
+    // the query fragments are re-read from LDS on every tile (an opaque index
+    // keeps them from being hoisted into registers)
+    int qo = lane;
+    asm volatile("" : "+v"(qo));
     f32x4 s = f32x4{};
 #pragma unroll
-    for (int k = 0; k < NKS; ++k) s = M::m16k32(kf[k], qf[k], s);
-    if (t + 1 < ntiles) load_tile(t + 1, blk_next, kf);
-    if (PAGE16) blk_next = tile_block(t + 2);
-
-    // scores: lane holds head column lane % 16, keys 4 grp + r of the tile
+    for (int k = 0; k < NKS; ++k) s = M::m16k32(__builtin_bit_cast(v8, kd[k]), qs[k * 64 + qo], s);
+    return s;
+  };
+  // second half: softmax of the scores (lane holds head column lane % 16,
+  // keys 4 grp + r of the tile) and O^T += V^T P^T
+  auto accumulate = [&](int t, f32x4 s) {
     const int64_t j0 = k_lo + 16 * (int64_t)t;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -452,6 +498,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void at
     const T* vp = vs + (4 * grp + (j16 >> 2)) * LDV + 4 * (j16 & 3);
 #pragma unroll
     for (int d = 0; d < NDT; ++d) oacc[d] = M::m16k16(tr4<v4>(vp + 16 * d), pf, oacc[d]);
+  };
+
+  // two tiles in flight: buffers A (even tiles) and B (odd tiles); block ids
+  // are looked up two tiles before their loads are issued.  Loads are issued
+  // unconditionally (a tile past the range reads zeros and its keys are
+  // masked), so no branch makes the compiler drain the loads in flight.
+  uint4 kA[NKS], kB[NKS];
+  uint4 vA[NLD], vB[NLD];
+  int64_t bA = tile_block(2), bB = tile_block(3);
+  load_tile(0, tile_block(0), kA, vA);
+  load_tile(1, tile_block(1), kB, vB);
+  for (int t = 0; t < ntiles; t += 2) {
+    f32x4 s = scores(kA, vA);
+    load_tile(t + 2, bA, kA, vA);
+    bA = tile_block(t + 4);
+    accumulate(t, s);
+    s = scores(kB, vB);
+    load_tile(t + 3, bB, kB, vB);
+    bB = tile_block(t + 5);
+    accumulate(t + 1, s);
   }
 
   float lt = lsum + __shfl_xor(lsum, 16);
@@ -564,11 +630,12 @@ int heads_per_group(int R) { return R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1); }
 template <typename T, int D>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t st) {
   const int hgroups = (a.Hq / a.Hkv + 15) / 16;
-  const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv * hgroups), (unsigned)a.B);
+  const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv / a.kvw * hgroups), (unsigned)a.B);
+  const size_t lds = (size_t)a.kvw * decode_lds_per_wave<T, D>();
   if (a.tab.page % 16 == 0)
-    hipLaunchKernelGGL((attn_decode_kernel<T, D, true>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, true>), grid, dim3(64 * a.kvw), lds, st, a);
   else
-    hipLaunchKernelGGL((attn_decode_kernel<T, D, false>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, false>), grid, dim3(64 * a.kvw), lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)((int64_t)a.B * a.Hq)), dim3(64), 0, st, a);
@@ -651,6 +718,7 @@ hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, c
   a.Hq = (int32_t)q->shape[1];
   a.Hkv = (int32_t)kc->shape[2];
   a.splits = splits;
+  a.kvw = a.Hkv % 4 == 0 ? 4 : (a.Hkv % 2 == 0 ? 2 : 1);
   a.c = scale * kLog2e;
   {
     const int64_t cap = a.tab.cols * (int64_t)a.tab.page;

@@ -21,7 +21,8 @@ import torch
 
 from . import _lib
 
-_DECODE_SPLIT_KEYS = 256
+_DECODE_MIN_SPLIT_KEYS = 256
+_DECODE_TARGET_WAVES = 2048
 _DECODE_MAX_SPLITS = 256
 
 
@@ -67,14 +68,15 @@ def flash_attention_prefill(
 def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int, capacity: int) -> int:
     """Key splits of the decode launch.  Split s covers keys [s c, (s+1) c) of
     the block table's ``capacity`` (max_blocks x page) with c = capacity /
-    splits, and splits past a sequence's length exit at once, so the splits
-    are what balances sequences of different lengths: about 256 keys per
-    split, fewer splits once the batch gives 16 split-rows of waves on its own
-    (more keys per wave, less partial-result traffic), at most 256."""
+    splits; splits past a sequence's length exit at once.  Enough splits for
+    about 2048 waves (8 per CU) over the batch's (sequence, kv head) rows,
+    but at least 256 keys per split and at most 256 splits: each split costs
+    a partial-result write and read, and on the batch-256 workload 4 splits
+    of 1024 keys beat 16 of 256."""
     rows = max(1, num_seqs * num_kv_heads * ((num_q_heads // max(num_kv_heads, 1) + 15) // 16))
-    by_keys = -(-max(capacity, 1) // _DECODE_SPLIT_KEYS)
-    by_waves = max(16, -(-8192 // rows))
-    return max(1, min(_DECODE_MAX_SPLITS, by_keys, by_waves))
+    by_waves = -(-_DECODE_TARGET_WAVES // rows)
+    by_keys = -(-max(capacity, 1) // _DECODE_MIN_SPLIT_KEYS)
+    return max(1, min(_DECODE_MAX_SPLITS, by_waves, by_keys))
 
 
 def paged_flash_attention_decode(
