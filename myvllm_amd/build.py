@@ -30,6 +30,10 @@ SOURCES = [
 ]
 
 ARCH = "gfx950"
+# Per-source flags.  attention.hip: keep MFMA accumulators in architectural
+# VGPRs; with the default AGPR form the D=256 prefill tile (128 accumulator
+# registers) was shuttled between AGPRs and VGPRs on every key tile.
+SOURCE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 # Packed-FP32 VALU ops are disabled for all device code (they are generated
 # from plain float2 arithmetic at -O3 otherwise).
 COMMON_FLAGS = [
@@ -78,7 +82,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     for src in SOURCES:
         obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         for f in [ex.submit(_run, c, verbose) for c in cmds]:

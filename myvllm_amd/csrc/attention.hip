@@ -168,24 +168,39 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     }
   }
 
-  uint4 kr[NLD], vr[NLD];
-  auto load_tile = [&](int t) {
+  // staging of a K/V tile: global rows -> registers (rows past kend read as
+  // zero, so a tile past the range loads nothing) -> LDS
+  // packed rows: buffer loads through descriptors of this sequence's kv-head
+  // rows [0, kend) (32-bit offsets; rows past kend read as zero)
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k.base + s0 * a.k.st + kvh * a.k.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.k.st), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v.base + s0 * a.v.st + kvh * a.v.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.v.st), 0x00020000);
+  auto load_tile = [&](int t, uint4* kd, uint4* vd) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int c = tid + 256 * i, row = c / CH, ch = c % CH;
       const int64_t j = (int64_t)t * BN + row;
+      if (!PAGED) {
+        // offsets past the descriptor's range (>= 2^31 > kend * stride) read zero
+        const uint32_t ko = j < kend ? (uint32_t)j * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
+        const uint32_t vo = j < kend ? (uint32_t)j * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
+        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+        continue;
+      }
       const char* pk = j < kend ? kv_row<PAGED>(a.k, a.tab, n, s0, j, kvh) : nullptr;
       const char* pv = j < kend ? kv_row<PAGED>(a.v, a.tab, n, s0, j, kvh) : nullptr;
-      kr[i] = pk ? *reinterpret_cast<const uint4*>(pk + 16 * ch) : uint4{0, 0, 0, 0};
-      vr[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+      kd[i] = pk ? *reinterpret_cast<const uint4*>(pk + 16 * ch) : uint4{0, 0, 0, 0};
+      vd[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, const uint4* kd, const uint4* vd) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int c = tid + 256 * i, row = c / CH, ch = c % CH;
-      *reinterpret_cast<uint4*>(&ks[buf][row * LDK + 8 * ch]) = kr[i];
-      *reinterpret_cast<uint4*>(&vs[buf][row * LDV + 8 * ch]) = vr[i];
+      *reinterpret_cast<uint4*>(&ks[buf][row * LDK + 8 * ch]) = kd[i];
+      *reinterpret_cast<uint4*>(&vs[buf][row * LDV + 8 * ch]) = vd[i];
     }
   };
 
@@ -195,14 +210,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   float m_used = -INFINITY, lsum = 0.f;
   const float c = a.c;
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
+  auto compute = [&](int t, int buf) {
     if ((int64_t)t * BN < kend_w) {
       const T* K = ks[buf];
       const T* V = vs[buf];
@@ -279,7 +287,24 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
         }
       }
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+  };
+
+  // tile t computes from LDS buffer t % 2 while tile t + 1 waits in registers
+  // and tile t + 2 is in flight: two register sets (A: even tiles, B: odd)
+  uint4 kA[NLD], vA[NLD], kB[NLD], vB[NLD];
+  load_tile(0, kA, vA);
+  store_tile(0, kA, vA);
+  load_tile(1, kB, vB);
+  load_tile(2, kA, vA);
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    compute(t, 0);
+    store_tile(1, kB, vB);
+    load_tile(t + 3, kB, vB);
+    __syncthreads();
+    compute(t + 1, 1);
+    store_tile(0, kA, vA);
+    load_tile(t + 4, kA, vA);
     __syncthreads();
   }
 

@@ -5,6 +5,8 @@
 // a machine with no GPU).  The reference ops validate nothing beyond a few
 // asserts (ops/gated_delta_rule/solve_tril.py:98, ops/gated_delta_rule/h.py:211).
 #include <hip/hip_runtime_api.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include "../../include/gdn_hip.h"
@@ -421,6 +423,9 @@ GDN_EXPORT int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, 
   const int64_t gh = R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1);
   if (cu_seqlens->shape[0] - 1 > kMaxGridYZ || q->shape[1] / gh > kMaxGridYZ || max_seqlen / 32 > kMaxGrid)
     return GDN_ERR_RANGE;
+  // a sequence's kv rows are addressed with 32-bit byte offsets below 2^31
+  const int64_t es = elem_size(k->dtype);
+  if (max_seqlen * std::max(k->stride[0], v->stride[0]) * es >= (int64_t(1) << 31)) return GDN_ERR_RANGE;
   return launch_rc(attn_varlen_prefill_launch(q, k, v, cu_seqlens, out, max_seqlen, scale, causal,
                                               reinterpret_cast<hipStream_t>(stream)));
 }
@@ -462,6 +467,10 @@ GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_c
   if (num_splits < 1 || num_splits > kMaxDecodeSplits) return GDN_ERR_RANGE;
   const int64_t Hkv = k_cache->shape[2], R = q->shape[1] / Hkv;
   if (B > kMaxGridYZ || Hkv * ((R + 15) / 16) > kMaxGridYZ) return GDN_ERR_RANGE;
+  // one page of one kv head is addressed with 32-bit byte offsets below 2^31
+  const int64_t es = elem_size(k_cache->dtype);
+  if (k_cache->shape[1] * std::max(k_cache->stride[1], v_cache->stride[1]) * es >= (int64_t(1) << 31))
+    return GDN_ERR_RANGE;
   float* ws = nullptr;
   if (num_splits > 1) {
     GDN_TRY(check_desc(workspace, 1));
