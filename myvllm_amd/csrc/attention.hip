@@ -167,6 +167,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       qf[s] = qvalid ? *reinterpret_cast<const v8*>(qp + 16 * s) : v8{};
     }
   }
+  // the softmax below assumes c > 0: a negative scale is folded into q (an
+  // exact sign flip), a zero scale is q = 0 with c = 1 (equal weights)
+  float c = a.c;
+  if (c <= 0.f) {
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) qf[s] = c < 0.f ? -qf[s] : v8{};
+    c = c < 0.f ? -c : 1.f;
+  }
 
   // staging of a K/V tile: global rows -> registers (rows past kend read as
   // zero, so a tile past the range loads nothing) -> LDS
@@ -208,7 +216,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 #pragma unroll
   for (int d = 0; d < NDT; ++d) oacc[d] = f32x16{};
   float m_used = -INFINITY, lsum = 0.f;
-  const float c = a.c;
 
   auto compute = [&](int t, int buf) {
     if ((int64_t)t * BN < kend_w) {
@@ -225,34 +232,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       // mask keys past the sequence / context and, if causal, past the query
       const int64_t tk0 = (int64_t)t * BN;
       if (tk0 + BN > Lk || (a.causal && tk0 + BN - 1 > off + q0)) {
-        const int64_t lim = a.causal ? (off + qi + 1 < Lk ? off + qi + 1 : Lk) : Lk;
+        const int64_t lim = (a.causal ? (off + qi + 1 < Lk ? off + qi + 1 : Lk) : Lk) - tk0;
+        const int rel = (int)clamp64(lim, -1, BN);  // keys of the tile at or past rel are masked
 #pragma unroll
         for (int aa = 0; aa < NA; ++aa)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t j = tk0 + 32 * aa + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (j >= lim) s[aa][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (32 * aa + 8 * (r >> 2) + 4 * hh + (r & 3) >= rel) s[aa][r] = -INFINITY;
       }
-      // tile maximum of the scaled scores (c may have either sign)
-      float mt = -INFINITY;
-      if (c >= 0.f) {
-        float mx = -INFINITY;
+      // tile maximum of the scaled scores (c > 0); masked scores are -inf and
+      // give p = exp2(-inf) = 0 below
+      float mx = -INFINITY;
 #pragma unroll
-        for (int aa = 0; aa < NA; ++aa)
+      for (int aa = 0; aa < NA; ++aa)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[aa][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        mt = mx == -INFINITY ? -INFINITY : mx * c;
-      } else {
-        float mn = INFINITY;
-#pragma unroll
-        for (int aa = 0; aa < NA; ++aa)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mn = s[aa][r] == -INFINITY ? mn : fminf(mn, s[aa][r]);
-        mn = fminf(mn, __shfl_xor(mn, 32));
-        mt = mn == INFINITY ? -INFINITY : mn * c;
-      }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[aa][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mt = mx * c;
       if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
         const float mn = fmaxf(m_used, mt);
         const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
@@ -269,8 +265,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           v8 pf;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float sv = s[aa][8 * h2 + e];
-            const float p = sv == -INFINITY ? 0.f : exp2_fast(__builtin_fmaf(sv, c, nb));
+            const float p = exp2_fast(__builtin_fmaf(s[aa][8 * h2 + e], c, nb));
             lsum += p;
             pf[e] = (T)p;
           }
@@ -394,8 +389,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   // dims 32 s + 8 grp .. +7; kept in LDS to leave registers for two tiles in flight
   {
     const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_ss + (int64_t)head * a.q_sh + 8 * grp;
+    // a negative scale is folded into q (an exact sign flip), a zero scale is
+    // q = 0 with c = 1 (equal weights), so the softmax below has c > 0
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) qs[s * 64 + lane] = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
+    for (int s = 0; s < NKS; ++s) {
+      const v8 qv = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
+      qs[s * 64 + lane] = a.c > 0.f ? qv : (a.c < 0.f ? -qv : v8{});
+    }
   }
 
   // block id of tile t's page (PAGE16), -1 past the range or for an entry
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
   for (int d = 0; d < NDT; ++d) oacc[d] = f32x4{};
   float m_used = -INFINITY, lsum = 0.f;
-  const float c = a.c;
+  const float c = a.c > 0.f ? a.c : (a.c < 0.f ? -a.c : 1.f);
 
   // first half of a tile: its V rows to LDS (the previous tile's transposed
   // reads were issued earlier by this wave, and LDS operations of a wave
@@ -488,20 +488,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (j0 + 4 * grp + r >= k_hi) s[r] = -INFINITY;
-    float mt;
-    if (c >= 0.f) {
-      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      mt = mx == -INFINITY ? -INFINITY : mx * c;
-    } else {
-      float mn = INFINITY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mn = s[r] == -INFINITY ? mn : fminf(mn, s[r]);
-      mn = fminf(mn, __shfl_xor(mn, 16));
-      mn = fminf(mn, __shfl_xor(mn, 32));
-      mt = mn == INFINITY ? -INFINITY : mn * c;
-    }
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mt = mx * c;  // c > 0; masked scores are -inf and give p = 0
     if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
       const float mn = fmaxf(m_used, mt);
       const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
@@ -514,7 +504,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     v4 pf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float p = s[r] == -INFINITY ? 0.f : exp2_fast(__builtin_fmaf(s[r], c, nb));
+      const float p = exp2_fast(__builtin_fmaf(s[r], c, nb));
       lsum += p;
       pf[r] = (T)p;
     }
