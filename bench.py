@@ -44,11 +44,13 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_050_890_969,
-    "gdn_recurrent_step_kernel": 1_083_200_285,
-    "causal_conv1d_varlen_kernel": 666_053_847,
-    "causal_conv1d_step_kernel": 59_313_267,
-    "gdn_decode_fused_kernel": 1_131_400_901,
+    "gdn_chunk_prefill_kernel": 1_051_147_331,
+    "gdn_recurrent_step_kernel": 1_083_221_975,
+    "causal_conv1d_varlen_kernel": 666_063_250,
+    "causal_conv1d_step_kernel": 59_315_355,
+    "gdn_decode_fused_kernel": 1_131_413_885,
+    "attn_prefill_kernel": 1_327_719_360,
+    "attn_decode_kernel": 1_253_246_826,
 }
 
 
@@ -382,7 +384,7 @@ def bench_attn_prefill(dev, steps, warmup, cpu_budget):
         "TFLOP_per_s": tflops,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / PEAK_MFMA_TFLOPS, "traffic": _traffic("attn_prefill_kernel"),
-                     "flops_per_launch": flops, "kernel": "attn_prefill_kernel"},
+                     "flop_per_launch": flops, "kernel": "attn_prefill_kernel"},
     }
     if cpu_budget > 0:
         from oracle.attention import attention_rows_ref
