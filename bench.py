@@ -9,8 +9,11 @@ recurrent decode step (batch 256, fp32 state gathered from a 1024-slot
 cache, HBM GB/s), the varlen causal conv1d (8 sequences, 19,762 tokens,
 8192 channels, width 4), the conv decode update (batch 256) and the fused
 decode step (conv update + L2 norm + gating + recurrent step, batch 256,
-with the same step as separate ops timed beside it), each with its
-roofline and, where it applies, the CPU oracle timed on this host.
+with the same step as separate ops timed beside it), and the neighbouring
+full-attention layers' causal varlen prefill (the same 16 sequence lengths,
+Hq 16 / Hkv 2, d 256) and paged decode (batch 256, contexts U[512, 4096],
+16-token pages), each with its roofline and, where it applies, the CPU
+oracle timed on this host.
 
 A step is one call of the op on inputs already resident in HBM.  Timing:
 W untimed warm-up steps, then K steps bracketed by device synchronisation;
