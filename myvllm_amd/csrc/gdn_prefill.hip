@@ -288,15 +288,20 @@ GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
 // of an off-diagonal block of the same T' buffer: row i's columns 0..15 in
 // the hi array, 16..31 in the lo array (64 bytes each, 8-byte aligned).
 struct Scratch {
-  char* hi;  // byte address of the block's row 0 in the hi array
-  char* lo;
-  GDN_DEVICE float* row(int i, int half) const { return reinterpret_cast<float*>((half ? lo : hi) + i * (2 * LDH)); }
+  // byte address of the block's row 0 in the hi array; the lo array follows
+  // the hi array at a fixed distance, so a lane-dependent half is an integer
+  // offset (a select between two pointers went through private memory and
+  // turned the LDS accesses into flat ones)
+  char* hi;
+  static constexpr int kLoOff = C * LDH * (int)sizeof(f16_t);
+  GDN_DEVICE float* row(int i, int half) const { return reinterpret_cast<float*>(hi + half * kLoOff + i * (2 * LDH)); }
   GDN_DEVICE float& at(int i, int j) const { return row(i, j >> 4)[j & 15]; }
 };
+static_assert(offsetof(TBuf, lo) == Scratch::kLoOff, "TBuf: lo follows hi");
 // diagonal block blk (0 or 1) of tb is worked on in its off-diagonal block (0,1) or (1,0)
 GDN_DEVICE Scratch scratch_of(TBuf& tb, int blk) {
   const int off = blk == 0 ? 32 : 32 * LDH;  // halves
-  return {reinterpret_cast<char*>(tb.hi + off), reinterpret_cast<char*>(tb.lo + off)};
+  return {reinterpret_cast<char*>(tb.hi + off)};
 }
 GDN_DEVICE f32x4 load4(const float* p) {
   const f32x2 a = *reinterpret_cast<const f32x2*>(p), b = *reinterpret_cast<const f32x2*>(p + 2);
