@@ -146,7 +146,7 @@ GDN_DEVICE void conv_tile(const ConvArgs& a, int64_t seq, int64_t tile, int64_t 
         for (int c = 0; c < kCh; ++c) y[c] *= sc;
       }
       if (r0 + u < nt)
-        Vec8<TX>::store(reinterpret_cast<TX*>(reinterpret_cast<char*>(ot) + (uint32_t)(r0 + u) * os * (uint32_t)sizeof(TX)), y);
+        store8_nt(reinterpret_cast<TX*>(reinterpret_cast<char*>(ot) + (uint32_t)(r0 + u) * os * (uint32_t)sizeof(TX)), y);
 #pragma unroll
       for (int m = 0; m < W - 2; ++m)
 #pragma unroll
