@@ -403,6 +403,42 @@ def bench_attn_prefill(dev, steps, warmup, cpu_budget):
     return res
 
 
+def bench_attn_paged_prefill(dev, steps, warmup, cpu_budget):
+    """Chunked prefill over a paged KV cache (16 sequences, cached prefixes
+    U[0, 4096], new chunks U[256, 2048], 16-token pages, Hq 16 / Hkv 2, D 256)."""
+    from myvllm_amd import paged_flash_attention_prefill
+    from myvllm_amd.workloads import ATTN_D, ATTN_HQ, attn_paged_prefill_case
+
+    case = attn_paged_prefill_case()
+    q, kc, vc, tab, ctx, cu = (t.to(dev) for t in (case.q, case.k_cache, case.v_cache, case.block_tables,
+                                                    case.context_lens, case.cu))
+    out = torch.empty_like(q)
+    max_len = case.max_len
+
+    def step(_):
+        paged_flash_attention_prefill(q, kc, vc, tab, ctx, cu, None, case.scale, case.page, max_seqlen=max_len,
+                                      out=out)
+
+    ms, kern_ms = _time_gpu(step, steps, warmup)
+    lens = (case.cu[1:] - case.cu[:-1]).tolist()
+    ctxs = case.context_lens.tolist()
+    pairs = sum(n * (L - n) + n * (n + 1) // 2 for n, L in zip(lens, ctxs))  # visible (query, key) pairs
+    flops = 4 * ATTN_D * ATTN_HQ * pairs
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    tokens = int(case.cu[-1])
+    return {
+        "tokens": tokens,
+        "cached_keys": int(sum(ctxs)),
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms,
+        "tokens_per_s": tokens / (kern_ms * 1e-3),
+        "TFLOP_per_s": tflops,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_MFMA_TFLOPS, "traffic": None, "flop_per_launch": flops,
+                     "kernel": "attn_prefill_kernel (paged)"},
+    }
+
+
 def bench_attn_decode(dev, steps, warmup, cpu_budget):
     """Paged decode of the attention layers: batch 256, contexts uniform in
     [512, 4096] (602,903 cached keys), 16-token pages, Hq 16, Hkv 2, D 256."""
@@ -482,7 +518,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="all",
                     help="all, or a comma-separated list of prefill, decode, conv, conv_update, decode_fused, "
-                         "layer, attn_prefill, attn_decode, hbm_copy")
+                         "layer, attn_prefill, attn_paged_prefill, attn_decode, hbm_copy")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     args = ap.parse_args()
@@ -497,8 +533,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill", "attn_decode",
-             "hbm_copy"}
+    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill",
+             "attn_paged_prefill", "attn_decode", "hbm_copy"}
     chosen = set(args.workload.split(","))
     if not chosen <= (known | {"all"}):
         print(f"unknown workload(s): {sorted(chosen - known - {'all'})}", file=sys.stderr)
@@ -532,6 +568,10 @@ def main():
         parts["attn_prefill"] = bench_attn_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# attn_prefill: {parts['attn_prefill']['kernel_ms'] * 1e3:.1f} us/launch "
               f"({parts['attn_prefill']['TFLOP_per_s']:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+    if want("attn_paged_prefill"):
+        parts["attn_paged_prefill"] = bench_attn_paged_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# attn_paged_prefill: {parts['attn_paged_prefill']['kernel_ms'] * 1e3:.1f} us/launch "
+              f"({parts['attn_paged_prefill']['TFLOP_per_s']:.0f} TFLOP/s)", file=sys.stderr, flush=True)
     if want("attn_decode"):
         parts["attn_decode"] = bench_attn_decode(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# attn_decode: {parts['attn_decode']['kernel_ms'] * 1e3:.1f} us/step "

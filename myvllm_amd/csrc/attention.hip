@@ -110,8 +110,12 @@ GDN_DEVICE const char* kv_row(const KvSource& s, const PagedTable& tb, int64_t n
 // (4 / gh) blocks of 32 queries.  K and V tiles of BN keys are staged in LDS
 // (double buffered, the next tile prefetched into registers) and shared by
 // the four waves.
-template <typename T, int D, int BN, bool PAGED>
+// PG: 0 packed rows, 1 paged (any page size: a table lookup per row),
+// 2 paged with a page size that is a multiple of 16 (one lookup per 16 rows,
+// through the scalar cache, so the data loads do not wait on vector loads)
+template <typename T, int D, int BN, int PG>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
+  constexpr bool PAGED = PG != 0;
   typedef Mma<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -184,11 +188,34 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       (void*)(a.k.base + s0 * a.k.st + kvh * a.k.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.k.st), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.v.base + s0 * a.v.st + kvh * a.v.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.v.st), 0x00020000);
+  constexpr int NG = BN / 16;  // 16-row groups of a tile
   auto load_tile = [&](int t, uint4* kd, uint4* vd) {
+    int64_t bl[NG];
+    if (PG == 2) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int64_t j0 = (int64_t)t * BN + 16 * g, col = j0 / a.tab.page;
+        int64_t blk = -1;
+        if (j0 < kend && col < a.tab.cols) blk = load_index_scalar(a.tab.table, n * a.tab.row_stride + col, a.tab.is64);
+        bl[g] = blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int c = tid + 256 * i, row = c / CH, ch = c % CH;
       const int64_t j = (int64_t)t * BN + row;
+      if (PG == 2) {
+        int64_t blk = bl[0];
+#pragma unroll
+        for (int g = 1; g < NG; ++g) blk = (row >> 4) == g ? bl[g] : blk;
+        const bool ok = j < kend && blk >= 0;
+        const int64_t slot = j % a.tab.page;
+        const char* pk = a.k.base + (ok ? blk * a.k.sb + slot * a.k.st + kvh * a.k.sh : 0);
+        const char* pv = a.v.base + (ok ? blk * a.v.sb + slot * a.v.st + kvh * a.v.sh : 0);
+        kd[i] = ok ? *reinterpret_cast<const uint4*>(pk + 16 * ch) : uint4{0, 0, 0, 0};
+        vd[i] = ok ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+        continue;
+      }
       if (!PAGED) {
         // offsets past the descriptor's range (>= 2^31 > kend * stride) read zero
         const uint32_t ko = j < kend ? (uint32_t)j * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
@@ -624,7 +651,12 @@ hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hi
   const int qsubs = 4 / a.gh;
   const int64_t qblocks = (max_len + 32 * qsubs - 1) / (32 * qsubs);
   const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)nseq);
-  hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, PAGED>), grid, dim3(256), 0, st, a);
+  if (!PAGED)
+    hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 0>), grid, dim3(256), 0, st, a);
+  else if (a.tab.page % 16 == 0)
+    hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 2>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 1>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

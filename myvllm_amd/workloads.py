@@ -277,3 +277,13 @@ def attn_decode_case(B: int = 256, seed: int = 0, page: int = 16, lo: int = 512,
     gen = torch.Generator().manual_seed(seed)
     ctx = torch.randint(lo, hi + 1, (B,), generator=gen).tolist()
     return paged_case(ctx, [1] * B, page=page, seed=seed + 1, **kw)
+
+
+def attn_paged_prefill_case(seed: int = 0, **kw) -> PagedCase:
+    """Chunked prefill over a paged cache: 16 sequences with a cached prefix
+    uniform in [0, 4096] and a new chunk uniform in [256, 2048] (whose keys are
+    already in the cache), 16-token pages."""
+    gen = torch.Generator().manual_seed(seed)
+    new = torch.randint(256, 2049, (16,), generator=gen)
+    prefix = torch.randint(0, 4097, (16,), generator=gen)
+    return paged_case((prefix + new).tolist(), new.tolist(), seed=seed + 1, **kw)
