@@ -16,8 +16,13 @@ Fixtures (safetensors, all tensors stored as written below):
 * gdn_decode_small.safetensors: batch 3 from a 4-slot cache, Hk 1 / Hv 2.
 * conv_varlen_small.safetensors / conv_update_small.safetensors: 64 channels,
   width 4, lengths [3, 1, 10, 0, 7] / batch 5.
+* attn_varlen_small.safetensors: causal varlen attention, lengths [1, 17, 40],
+  Hq 4 / Hkv 2, d 64, bf16 inputs, fp32 output.
+* attn_paged_small.safetensors: paged prefill (contexts [20, 7, 33], new
+  [3, 7, 1], 8-token pages) and paged decode (contexts [20, 1, 40]) over one
+  cache, Hq 4 / Hkv 2, d 64, bf16 inputs, fp32 outputs.
 
-Run from the repository root: python tests/golden/make_golden.py
+Run from the repository root: python tests/golden/make_golden.py [name ...]
 """
 from __future__ import annotations
 
@@ -31,7 +36,17 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-from myvllm_amd.workloads import conv_decode_case, conv_prefill_case, decode_case, gdn_inputs, prefill_case  # noqa: E402
+from myvllm_amd.workloads import (  # noqa: E402
+    attn_varlen_case,
+    conv_decode_case,
+    conv_prefill_case,
+    cu_from_lengths,
+    decode_case,
+    gdn_inputs,
+    paged_case,
+    prefill_case,
+)
+from oracle.attention import flash_attention_prefill_ref, paged_attention_ref  # noqa: E402
 from oracle.conv import causal_conv1d_fn_ref, causal_conv1d_update_ref  # noqa: E402
 from oracle.gdn import chunk_gated_delta_rule_ref, recurrent_gated_delta_rule_ref  # noqa: E402
 
@@ -79,17 +94,42 @@ def conv_update_small():
             "y": y.float().contiguous(), "final_state": st}
 
 
+def attn_varlen_small():
+    c = attn_varlen_case([1, 17, 40], seed=8, Hq=4, Hkv=2, D=64)
+    o = flash_attention_prefill_ref(c.q, c.k, c.v, c.cu, c.scale, is_causal=True)
+    return {"q": c.q, "k": c.k, "v": c.v, "cu_seqlens": c.cu, "scale": torch.tensor([c.scale]),
+            "o": o.float().contiguous()}
+
+
+def attn_paged_small():
+    c = paged_case([20, 7, 33], [3, 7, 1], page=8, seed=9, Hq=4, Hkv=2, D=64)
+    o = paged_attention_ref(c.q, c.k_cache, c.v_cache, c.block_tables, c.context_lens, c.cu, c.scale)
+    # decode over the same cache: one query per sequence at position ctx - 1
+    dctx = torch.tensor([20, 1, 40], dtype=torch.int32)
+    dq = torch.randn(3, 4, 64, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    # (sequence 2's five pages hold 40 keys: the 33 of the prefill and 7 more cache rows)
+    od = paged_attention_ref(dq, c.k_cache, c.v_cache, c.block_tables, dctx, cu_from_lengths([1, 1, 1]), c.scale)
+    return {"q": c.q, "k_cache": c.k_cache, "v_cache": c.v_cache, "block_tables": c.block_tables,
+            "context_lens": c.context_lens, "cu_seqlens": c.cu, "scale": torch.tensor([c.scale]),
+            "o": o.float().contiguous(), "decode_q": dq, "decode_context_lens": dctx,
+            "decode_o": od.float().contiguous()}
+
+
 FIXTURES = {
     "gdn_recurrent_64tok": recurrent_64tok,
     "gdn_chunk_varlen_small": chunk_varlen_small,
     "gdn_decode_small": decode_small,
     "conv_varlen_small": conv_varlen_small,
     "conv_update_small": conv_update_small,
+    "attn_varlen_small": attn_varlen_small,
+    "attn_paged_small": attn_paged_small,
 }
 
 
 def main():
-    for name, fn in FIXTURES.items():
+    names = sys.argv[1:] or list(FIXTURES)
+    for name in names:
+        fn = FIXTURES[name]
         tensors = {k: v.contiguous() for k, v in fn().items()}
         path = os.path.join(HERE, name + ".safetensors")
         save_file(tensors, path)

@@ -6,7 +6,8 @@ import torch
 from safetensors.torch import load_file
 
 from conftest import assert_out_close, assert_state_close
-from myvllm_amd import causal_conv1d_fn, causal_conv1d_update, chunk_gated_delta_rule, recurrent_gated_delta_rule
+from myvllm_amd import (causal_conv1d_fn, causal_conv1d_update, chunk_gated_delta_rule, flash_attention_prefill,
+                        paged_flash_attention_decode, paged_flash_attention_prefill, recurrent_gated_delta_rule)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -56,3 +57,18 @@ def test_golden_conv(dev):
     y = causal_conv1d_update(f["x"], f["weight"], st, f["state_indices"])
     assert_out_close(y, f["y"])
     assert torch.equal(st, f["final_state"])
+
+
+def test_golden_attention(dev):
+    f = _load("attn_varlen_small", dev)
+    o = flash_attention_prefill(f["q"], f["k"], f["v"], f["cu_seqlens"], float(f["scale"]), 4, 2, 64, 64, True)
+    assert_out_close(o, f["o"])
+    f = _load("attn_paged_small", dev)
+    page = f["k_cache"].shape[1]
+    o = paged_flash_attention_prefill(f["q"], f["k_cache"], f["v_cache"], f["block_tables"], f["context_lens"],
+                                      f["cu_seqlens"], None, float(f["scale"]), page)
+    assert_out_close(o, f["o"])
+    for splits in (1, 3):
+        od = paged_flash_attention_decode(f["decode_q"], f["k_cache"], f["v_cache"], f["block_tables"],
+                                          f["decode_context_lens"], float(f["scale"]), page, num_splits=splits)
+        assert_out_close(od, f["decode_o"])

@@ -300,6 +300,22 @@ def test_golden_conv():
     assert (y.float() - f["y"]).abs().max() < 1e-3 and torch.equal(st, f["final_state"])
 
 
+def test_golden_attention():
+    from oracle.attention import flash_attention_prefill_ref, paged_attention_ref
+    from myvllm_amd.workloads import cu_from_lengths
+
+    f = load_file(os.path.join(GOLDEN, "attn_varlen_small.safetensors"))
+    o = flash_attention_prefill_ref(f["q"], f["k"], f["v"], f["cu_seqlens"], float(f["scale"]), is_causal=True)
+    assert (o.float() - f["o"]).abs().max() < 1e-6
+    f = load_file(os.path.join(GOLDEN, "attn_paged_small.safetensors"))
+    o = paged_attention_ref(f["q"], f["k_cache"], f["v_cache"], f["block_tables"], f["context_lens"],
+                            f["cu_seqlens"], float(f["scale"]))
+    assert (o.float() - f["o"]).abs().max() < 1e-6
+    od = paged_attention_ref(f["decode_q"], f["k_cache"], f["v_cache"], f["block_tables"], f["decode_context_lens"],
+                             cu_from_lengths([1, 1, 1]), float(f["scale"]))
+    assert (od.float() - f["decode_o"]).abs().max() < 1e-6
+
+
 def test_workload_lengths_match_the_benchmark_description():
     from myvllm_amd.workloads import conv_prefill_case as cp, prefill_32k_case
 
