@@ -47,13 +47,13 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_051_147_331,
-    "gdn_recurrent_step_kernel": 1_083_221_975,
-    "causal_conv1d_varlen_kernel": 666_063_250,
-    "causal_conv1d_step_kernel": 59_315_355,
-    "gdn_decode_fused_kernel": 1_131_413_885,
-    "attn_prefill_kernel": 1_327_719_360,
-    "attn_decode_kernel": 1_253_246_826,
+    "gdn_chunk_prefill_kernel": 1_027_955_545,
+    "gdn_recurrent_step_kernel": 1_083_192_613,
+    "causal_conv1d_varlen_kernel": 665_982_052,
+    "causal_conv1d_step_kernel": 59_313_677,
+    "gdn_decode_fused_kernel": 1_131_474_927,
+    "attn_prefill_kernel": 1_327_165_005,
+    "attn_decode_kernel": 1_253_252_670,
 }
 
 
