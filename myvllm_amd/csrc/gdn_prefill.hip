@@ -867,7 +867,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     return;
   }
   const int nc = (int)((e - s + C - 1) / C);
-  auto chunk_len = [&](int c) { const int64_t r = e - (s + (int64_t)c * C); return (int)(r < C ? r : C); };
+  auto chunk_len = [&](int c) __attribute__((always_inline)) { const int64_t r = e - (s + (int64_t)c * C); return (int)(r < C ? r : C); };
 
   // Both roles execute exactly 1 + nc workgroup barriers.
   if (wave < 4) {
@@ -906,14 +906,14 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   // everything else of chunk 0.
   const int pw = wave - 4;
   const ChunkSource src = {&a, a.k + kh * a.k_s1, a.q + kh * a.q_s1, a.v + h * a.v_s1, h, e};
-  auto c0_of = [&](int c) { return s + (int64_t)c * C; };
+  auto c0_of = [&](int c) __attribute__((always_inline)) { return s + (int64_t)c * C; };
   if (pw < 2) {
     float* dgam = sm.dvec[pw][0];
     float* dbeta = sm.dvec[pw][1];
     DiagLoad dl;
     // solve this wave's diagonal block of chunk c (its loads are in dl) into
     // T' buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
-    auto solve = [&](int c) {
+    auto solve = [&](int c) __attribute__((always_inline)) {
       float gl;
       const int L = chunk_len(c);
       dgam[lane] = chunk_gamma(dl.d, L, lane, gl);
@@ -935,19 +935,19 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   } else if (pw == 2) {
     TileLoad kl;
     DecayLoad dl;
-    auto load = [&](int c) {
+    auto load = [&](int c) __attribute__((always_inline)) {
       const int Lc = chunk_rows(src, c0_of(c));
       load_tile(kl, src.kg, a.k_s0, c0_of(c), Lc, lane);
       load_decay(dl, src, c0_of(c), Lc, lane);
     };
     // K tile and decay vectors of chunk c into tile set c & 1, then release wave 7
-    auto stage = [&](int c) {
+    auto stage = [&](int c) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[c & 1];
       stage_f16(ct.k, kl, lane);
       stage_decay(ct, dl, chunk_len(c), a.b_dtype, lane);
       producer_arrive(&sm.kv_ready, lane);
     };
-    auto offdiag = [&](int c) {
+    auto offdiag = [&](int c) __attribute__((always_inline)) {
       b10_block(sm.tiles[c & 1], sm.tb[c % 3], lane);
       merge_offdiag(sm.tb[c % 3], lane);
     };
@@ -968,10 +968,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     }
   } else {
     TileLoad ql, vl;
-    auto qload = [&](int c) { load_tile(ql, src.qg, a.q_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
-    auto vload = [&](int c) { load_tile(vl, src.vg, a.v_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
+    auto qload = [&](int c) __attribute__((always_inline)) { load_tile(ql, src.qg, a.q_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
+    auto vload = [&](int c) __attribute__((always_inline)) { load_tile(vl, src.vg, a.v_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
     // Q tile and the three P tiles of chunk c
-    auto qp = [&](int c) {
+    auto qp = [&](int c) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[c & 1];
       stage_f16(ct.q, ql, lane);
       if (c + 1 < nc) qload(c + 1);
