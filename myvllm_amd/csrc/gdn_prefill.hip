@@ -34,7 +34,7 @@
 // values, which fp16 holds exactly, and every fp32 operand that feeds the
 // carried state (S, R, the decayed V', T', B_10 and the merge product) is
 // split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  S, R
-// and V' are first scaled by a per-wave power of two (max |x| in
+// and V' are first scaled by a power of two per value column (max |x| in
 // [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
 // undone on the fp32 accumulator.  The T' blocks and B_10 (|B_10| <= 1) are
 // split unscaled.  Products that only feed o use the hi part.
@@ -52,7 +52,6 @@
 namespace {
 
 constexpr int kThreads = 512;        // 4 state waves + 4 producer waves
-constexpr int kRoleThreads = 256;    // threads per role
 constexpr int C = 64;      // chunk
 constexpr int KD = 128;    // key head dim
 constexpr int VD = 128;    // value head dim
@@ -63,6 +62,7 @@ constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this ma
 constexpr int kSpinLimit = 1 << 22;  // bound on a producer barrier wait (never reached when correct)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -160,25 +160,14 @@ GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
 }
 
-// Maximum over the wave of a non-negative float, on every lane: DPP steps
-// within each 16-lane row (xor 1, xor 2, half-row and row mirrors), then the
-// four row results through scalar registers.  Non-negative floats order like
-// their bit patterns, so the maxima are taken on integers.
-GDN_DEVICE float wave_max_nonneg(float x) {
-  int v = __builtin_bit_cast(int, x);
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));  // row_mirror
-  const int r = max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-                    max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-  return __builtin_bit_cast(float, r);
-}
-
-// Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over the wave's
-// `nt` C tiles (0 when all are zero); the same on every lane.  The per-lane
-// maximum is a tree, so its latency is a few dependent operations.
-GDN_DEVICE int wave_scale_exp(const f32x16* t, int nt) {
+// Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over one value
+// column of the wave's `nt` C tiles (0 when all are zero).  In the C layout
+// lanes l and l ^ 32 hold the two row halves of column l % 32, so the
+// per-lane maximum (a tree of a few dependent operations) needs one exchange
+// between the wave halves; no wave-wide reduction.  Non-negative floats
+// order like their bit patterns, so the exchange takes the maximum on
+// integers.
+GDN_DEVICE int col_scale_exp(const f32x16* t, int nt) {
   float m[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -189,7 +178,9 @@ GDN_DEVICE int wave_scale_exp(const f32x16* t, int nt) {
   for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
     for (int j = 0; j < w; ++j) m[j] = fmaxf(m[j], m[j + w]);
-  const float mx = wave_max_nonneg(m[0]);
+  const uint32_t v = __builtin_bit_cast(uint32_t, m[0]);
+  const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const float mx = __builtin_bit_cast(float, max(sw[0], sw[1]));
   return mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 10 : 0;
 }
 
@@ -673,21 +664,30 @@ GDN_DEVICE void stage_decay(ChunkTiles& ct, const DecayLoad& dl, int L, int b_dt
 
 // ---- state role (waves 0..3) -----------------------------------------------------
 
+// Slot (0..7, 4 rows each) of a 32-row half of output column m in the output
+// staging: slot s is permuted by m / 4 with bits 1 and 2 of m / 4 swapped, so
+// the 32 columns of one 8-byte write and the column groups of one transposed
+// read each land in distinct banks.
+GDN_DEVICE int out_slot(int s, int m) {
+  const int q = (m >> 2) & 7;
+  return s ^ (((q & 2) << 1) | ((q & 4) >> 1) | (q & 1));
+}
+
 // The state products of one chunk on this wave's 32 value columns; writes the
 // chunk's output rows for those columns (staged through its own columns of
 // the V tile, after which it signals v_free).  The state is held in units of
-// 2^su (true state = S * 2^su, su wave-uniform): the update rescales S by
-// one factor per chunk and re-bases su on the exponent of V', so no other
-// pass over S is needed for the fp16 splits.
+// 2^su (true state = S * 2^su; su is per value column, since no product
+// mixes value columns): the update rescales S by one factor per chunk and
+// re-bases su on the exponent of V', so no other pass over S is needed for
+// the fp16 splits.
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, int32_t* v_free, f32x16 (&S)[4],
                               int& su, const PrefillArgs& a, int64_t c0, int L, int h, int wave, int lane) {
   // Lane-dependent addresses are cheap to recompute; keeping them out of
   // loop-invariant code motion keeps them out of registers across chunks.
   asm volatile("" : "+v"(lane));
   const int n = lane & 31, gq = lane >> 5;
-  const int col = 32 * wave + n;
   // X = K S, QS = Q S on the split of S 2^-es (true values: X 2^(es + su))
-  const int es = wave_scale_exp(S, 4);
+  const int es = col_scale_exp(S, 4);
   const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
   f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
 #pragma unroll
@@ -722,7 +722,7 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   }
   f32x16* R = X;  // X now holds R
   // (er >= ex - 100 keeps 2^(ex - er) finite; a smaller R is negligible next to the state)
-  const int er = max(wave_scale_exp(R, 2), ex - 100);
+  const int er = max(col_scale_exp(R, 2), ex - 100);
   const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
   // V' = T' R, in units of 2^er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
   f32x16 VN[2] = {zero16(), zero16()};
@@ -768,23 +768,38 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
 #pragma unroll
     for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(ct.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
   }
-  // stage this wave's output columns (bf16) in the V tile, then store 16-byte row pieces
+  // Stage this wave's output columns (bf16) in its own columns of the V tile,
+  // column-major: output column m's rows 32 h .. 32 h + 31 sit in tile row
+  // 2 m + h, in eight 4-row slots permuted by out_slot (conflict-free 8-byte
+  // writes and transposed reads).  Each lane writes 4 consecutive rows of its
+  // column at once, then reads back 16-byte row pieces with transposed reads.
   {
     const float osc = __builtin_amdgcn_ldexpf(a.scale, er);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int row = 32 * mt + 8 * (jj >> 2) + 4 * gq + (jj & 3);
-        vt[row * LDV + col] = (bf16_t)(QS[mt][jj] * osc);
+      for (int i = 0; i < 4; ++i) {
+        bf16x4 o4;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o4[rr] = (bf16_t)(QS[mt][4 * i + rr] * osc);
+        *reinterpret_cast<bf16x4*>(vt + (2 * n + mt) * LDV + 32 * wave + 4 * out_slot(2 * i + gq, n)) = o4;
       }
-    bf16_t* ob = a.out + c0 * a.o_s0 + h * a.o_s1 + 32 * wave;
+    // lane (qd, j) of the four 16-lane groups: output row 16 u + j, columns 8 qd .. 8 qd + 7
+    const int j = lane & 15, qd = lane >> 4;
+    bf16_t* ob = a.out + c0 * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * qd;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int row = 16 * u + (lane >> 2), cgp = lane & 3;
+      s16x4 half[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int m = 8 * qd + 4 * hh + (j >> 2);  // output column of this lane's address
+        half[hh] = tr_read(vt + (2 * m + (u >> 1)) * LDV + 32 * wave + 4 * out_slot(4 * (u & 1) + (j & 3), m));
+      }
+      const int row = 16 * u + j;
       if (row < L)
-        *reinterpret_cast<bf16x8*>(reinterpret_cast<char*>(ob) + ((uint32_t)row * (uint32_t)a.o_s0 + 8u * cgp) * 2u) =
-            *reinterpret_cast<const bf16x8*>(vt + row * LDV + 32 * wave + 8 * cgp);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(ob) + (uint32_t)row * (uint32_t)a.o_s0 * 2u) =
+            __builtin_bit_cast(u32x4, (s16x8){half[0][0], half[0][1], half[0][2], half[0][3],
+                                               half[1][0], half[1][1], half[1][2], half[1][3]});
     }
   }
   // this wave is done with the V tile (its values, then its output staging)
@@ -794,17 +809,17 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   // edec <= 1), and the new state is held in units of 2^ed:
   //   S' = S e^gamma_L 2^(su - ed) + K^T (Vd 2^-ed).
   // ed >= ex - 64 keeps S' far inside the fp32 range; evn >= -100 keeps 2^(er - ed) finite.
-  const int ed = max(er + max(wave_scale_exp(VN, 2), -100), ex - 64);
+  const int ed = max(er + max(col_scale_exp(VN, 2), -100), ex - 64);
   const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
   const float edl = __expf(ct.gam_last);
   const int dsu = su - ed;
-  if (dsu >= -100 && dsu <= 100) {
+  if (__builtin_amdgcn_ballot_w64(dsu < -100 || dsu > 100) == 0) {
     const float sdec = __builtin_amdgcn_ldexpf(edl, dsu);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] *= sdec;
-  } else {  // a factor outside the fp32 range: scale element by element
+  } else {  // a factor outside the fp32 range on some column: scale element by element
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
