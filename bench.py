@@ -13,7 +13,9 @@ with the same step as separate ops timed beside it), and the neighbouring
 full-attention layers' causal varlen prefill (the same 16 sequence lengths,
 Hq 16 / Hkv 2, d 256) and paged decode (batch 256, contexts U[512, 4096],
 16-token pages), each with its roofline and, where it applies, the CPU
-oracle timed on this host.
+oracle timed on this host.  Beside the datasheet peaks, the default run
+measures two ceilings of this device (a bf16 8192^3 GEMM through hipBLASLt and
+a 1 GiB copy) and gives each roofline as a fraction of the matching one too.
 
 A step is one call of the op on inputs already resident in HBM.  Timing:
 W untimed warm-up steps, then K steps bracketed by device synchronisation;
@@ -511,6 +513,22 @@ def bench_hbm_copy(dev, steps, warmup, cpu_budget):
                          "kernel": "torch elementwise copy"}}
 
 
+def measure_peaks(dev, steps, warmup):
+    """Ceilings measured on this device beside the datasheet peaks: a large
+    bf16 GEMM through torch (hipBLASLt) and a 1 GiB device-to-device copy."""
+    n = 8192
+    gen = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=gen)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=gen)
+    c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    _, kern_ms = _time_gpu(lambda _: torch.matmul(a, b, out=c), steps, warmup)
+    gemm = 2 * n ** 3 / (kern_ms * 1e-3) / 1e12
+    del a, b, c
+    copy = bench_hbm_copy(dev, steps, warmup, 0)["GB_per_s"]
+    return {"gemm_bf16_TFLOP_per_s": gemm, "gemm": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt)",
+            "copy_GB_per_s": copy, "copy": "torch copy_ of 1 GiB (read + write counted)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -578,6 +596,19 @@ def main():
               f"({parts['attn_decode']['GB_per_s']:.0f} GB/s)", file=sys.stderr, flush=True)
     if "hbm_copy" in chosen:
         parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
+    peaks = None
+    if "all" in chosen:
+        # each MFMA-bound roofline also as a fraction of a measured library GEMM,
+        # each HBM-bound one as a fraction of the measured copy rate
+        peaks = measure_peaks(dev, min(args.steps, 20), min(args.warmup, 5))
+        for part in parts.values():
+            roof = part.get("roofline")
+            if roof and roof["bound"] == "mfma":
+                roof["frac_of_measured_gemm"] = roof["achieved"] / peaks["gemm_bf16_TFLOP_per_s"]
+            elif roof and roof["bound"] == "hbm":
+                roof["frac_of_measured_copy"] = roof["achieved"] / peaks["copy_GB_per_s"]
+        print(f"# measured peaks: GEMM {peaks['gemm_bf16_TFLOP_per_s']:.0f} TFLOP/s, "
+              f"copy {peaks['copy_GB_per_s']:.0f} GB/s", file=sys.stderr, flush=True)
 
     head_name = "prefill" if "prefill" in parts else next(iter(parts))
     head = parts.pop(head_name)
@@ -627,6 +658,8 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
     }
+    if peaks is not None:
+        line["measured_peaks"] = peaks
     for name, part in parts.items():
         line[name] = part
     print(json.dumps(line))
