@@ -33,11 +33,13 @@
 // The MFMAs run in fp16 (same rate as bf16): q and k are L2-normalised bf16
 // values, which fp16 holds exactly, and every fp32 operand that feeds the
 // carried state (S, R, the decayed V', T', B_10 and the merge product) is
-// split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  S, R
+// split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  R
 // and V' are first scaled by a power of two per value column (max |x| in
 // [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
-// undone on the fp32 accumulator.  The T' blocks and B_10 (|B_10| <= 1) are
-// split unscaled.  Products that only feed o use the hi part.
+// undone on the fp32 accumulator.  The state is held in power-of-two units
+// per value column that keep |S| < 2^14, so it is split as it stands.  The
+// T' blocks and B_10 (|B_10| <= 1) are split unscaled.  Products that only
+// feed o use the hi part.
 //
 // MFMA operand layouts (lane l, n = l % 32, g = l / 32), 32x32x16:
 // A[m][k] lane holds row n, 8 k; B[k][n] lane holds column n, 8 k; C lane
@@ -160,14 +162,14 @@ GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
 }
 
-// Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over one value
-// column of the wave's `nt` C tiles (0 when all are zero).  In the C layout
-// lanes l and l ^ 32 hold the two row halves of column l % 32, so the
-// per-lane maximum (a tree of a few dependent operations) needs one exchange
-// between the wave halves; no wave-wide reduction.  Non-negative floats
-// order like their bit patterns, so the exchange takes the maximum on
-// integers.
-GDN_DEVICE int col_scale_exp(const f32x16* t, int nt) {
+// Exponent E with max|x| in [2^(E-1), 2^E) over one value column of the
+// wave's `nt` C tiles, kNone when the column is zero.  In the C layout lanes
+// l and l ^ 32 hold the two row halves of column l % 32, so the per-lane
+// maximum (a tree of a few dependent operations) needs one exchange between
+// the wave halves; no wave-wide reduction.  Non-negative floats order like
+// their bit patterns, so the exchange takes the maximum on integers.
+constexpr int kNone = -4096;
+GDN_DEVICE int col_max_exp(const f32x16* t, int nt) {
   float m[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -181,7 +183,14 @@ GDN_DEVICE int col_scale_exp(const f32x16* t, int nt) {
   const uint32_t v = __builtin_bit_cast(uint32_t, m[0]);
   const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
   const float mx = __builtin_bit_cast(float, max(sw[0], sw[1]));
-  return mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 10 : 0;
+  return mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : kNone;
+}
+
+// Power-of-two exponent e with max|x| * 2^-e in [2^9, 2^10) over one value
+// column (0 when the column is zero).
+GDN_DEVICE int col_scale_exp(const f32x16* t, int nt) {
+  const int e = col_max_exp(t, nt);
+  return e == kNone ? 0 : e - 10;
 }
 
 // Inclusive prefix sum over the 64 lanes (DPP row shifts, then the row
@@ -244,6 +253,21 @@ GDN_DEVICE void split8(const f32x16& c, int h, float sc, f16x8& hi, f16x8& lo) {
   for (int m = 0; m < 4; ++m) {
     H[m] = mix_hi_pair(c[8 * h + 2 * m], sc, c[8 * h + 2 * m + 1], sc);
     L[m] = mix_lo_pair(c[8 * h + 2 * m], sc, c[8 * h + 2 * m + 1], sc, H[m]);
+  }
+  hi = __builtin_bit_cast(f16x8, (u32x4){H[0], H[1], H[2], H[3]});
+  lo = __builtin_bit_cast(f16x8, (u32x4){L[0], L[1], L[2], L[3]});
+}
+// the same unscaled: hi = fp16(x), lo = fp16(fma(x, one, -hi)) with one = 1
+// held opaque by the caller (the compiler would otherwise fold the fma into a
+// subtraction and convert hi back to fp32 first)
+GDN_DEVICE void split8u(const f32x16& c, int h, float one, f16x8& hi, f16x8& lo) {
+  uint32_t H[4], L[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const f16x2 hv = {(f16_t)c[8 * h + 2 * m], (f16_t)c[8 * h + 2 * m + 1]};
+    H[m] = __builtin_bit_cast(uint32_t, hv);
+    asm volatile("" : "+v"(H[m]));
+    L[m] = mix_lo_pair(c[8 * h + 2 * m], one, c[8 * h + 2 * m + 1], one, H[m]);
   }
   hi = __builtin_bit_cast(f16x8, (u32x4){H[0], H[1], H[2], H[3]});
   lo = __builtin_bit_cast(f16x8, (u32x4){L[0], L[1], L[2], L[3]});
@@ -678,22 +702,23 @@ GDN_DEVICE int out_slot(int s, int m) {
 // the V tile, after which it signals v_free).  The state is held in units of
 // 2^su (true state = S * 2^su; su is per value column, since no product
 // mixes value columns): the update rescales S by one factor per chunk and
-// re-bases su on the exponent of V', so no other pass over S is needed for
-// the fp16 splits.
+// picks the new units from the exponents of V' and of the decayed state, so
+// S stays below 2^14 and is split without another pass over it.
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, int32_t* v_free, f32x16 (&S)[4],
                               int& su, const PrefillArgs& a, int64_t c0, int L, int h, int wave, int lane) {
   // Lane-dependent addresses are cheap to recompute; keeping them out of
   // loop-invariant code motion keeps them out of registers across chunks.
   asm volatile("" : "+v"(lane));
   const int n = lane & 31, gq = lane >> 5;
-  // X = K S, QS = Q S on the split of S 2^-es (true values: X 2^(es + su))
-  const int es = col_scale_exp(S, 4);
-  const float ss = __builtin_amdgcn_ldexpf(1.f, -es);
+  // X = K S, QS = Q S on the split of S itself (the choice of units below
+  // keeps |S| < 2^14, so fp16 cannot overflow; true values: X 2^su)
   f32x16 X[2] = {zero16(), zero16()}, QS[2] = {zero16(), zero16()};
+  float one = 1.f;  // opaque, so lo = fp16(fma(x, one, -hi)) stays one mixed-precision fma
+  asm volatile("" : "+v"(one));
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     f16x8 shi, slo;
-    split8(S[ks >> 1], ks & 1, ss, shi, slo);
+    split8u(S[ks >> 1], ks & 1, one, shi, slo);
     const f16x8 ak0 = frag_rows(ct.k, LDK, 0, 16 * ks, lane);
     const f16x8 ak1 = frag_rows(ct.k, LDK, 32, 16 * ks, lane);
     const f16x8 aq0 = frag_rows(ct.q, LDK, 0, 16 * ks, lane);
@@ -705,7 +730,9 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
     X[0] = mfma32(ak0, slo, X[0]);
     X[1] = mfma32(ak1, slo, X[1]);
   }
-  const int ex = es + su;
+  const int ex = su;
+  // exponent of this column's state maximum (max |S| < 2^sm), for the next units
+  const int sm = col_max_exp(S, 4);
   // R = V - diag(e^gamma) X in true units (V read transposed: rows are tokens)
   const float xu = __builtin_amdgcn_ldexpf(1.f, ex);
 #pragma unroll
@@ -804,14 +831,23 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   }
   // this wave is done with the V tile (its values, then its output staging)
   producer_arrive(v_free, lane);
-  // S_true' = e^gamma_L S_true + K^T Vd, Vd = diag(e^(gamma_L - gamma)) V' = diag(edec) VN 2^er.
-  // The split operand is Vd 2^-ed with ed = er + evn (max |VN| 2^-evn in [2^9, 2^10),
-  // edec <= 1), and the new state is held in units of 2^ed:
-  //   S' = S e^gamma_L 2^(su - ed) + K^T (Vd 2^-ed).
-  // ed >= ex - 64 keeps S' far inside the fp32 range; evn >= -100 keeps 2^(er - ed) finite.
-  const int ed = max(er + max(col_scale_exp(VN, 2), -100), ex - 64);
-  const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
+  // S_true' = e^gamma_L S_true + K^T Vd, Vd = diag(e^(gamma_L - gamma)) V' = diag(edec) VN 2^er,
+  // with the new state in units of 2^ed:  S' = S e^gamma_L 2^(su - ed) + K^T (Vd 2^-ed).
+  // ed keeps the split of S' (next chunk, unscaled) inside the fp16 range:
+  //  * the update: with max |VN| < 2^vm and edec <= 1 the split operand
+  //    Vd 2^-ed is below 2^(vm + er - ed) <= 2^6 when ed >= er + vm - 6, so
+  //    the update is below 2^6 sum_t |k_t|: 2^12 for L2-normalised keys
+  //    (|k| <= 1), and below 2^15 for any |k| <= 8;
+  //  * the decayed state: with max |S| < 2^sm and e^gamma_L < 2^lm it is below
+  //    2^(sm + lm + su - ed) <= 2^13 when ed >= sm + lm + su - 13;
+  // so |S'| < 2^13 + 2^12 (and < 2^15 + 2^13 < 65504 for |k| <= 8).  A part
+  // that is zero (sm, vm or lm = kNone) sets no bound; ed >= er - 100 keeps
+  // 2^(er - ed) finite.
   const float edl = __expf(ct.gam_last);
+  const int vm = col_max_exp(VN, 2);
+  const int lm = edl > 0.f ? __builtin_amdgcn_frexp_expf(edl) : kNone;
+  const int ed = max(max(er + vm - 6, sm + lm + su - 13), er - 100);
+  const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
   const int dsu = su - ed;
   if (__builtin_amdgcn_ballot_w64(dsu < -100 || dsu > 100) == 0) {
     const float sdec = __builtin_amdgcn_ldexpf(edl, dsu);
@@ -891,11 +927,19 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     const int col = 32 * wave + n;
     float* Sg = a.state + slot * a.st_slot + h * a.st_head;
     f32x16 S[4];
-    int su = 0;  // state units: true state = S * 2^su
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
+    // state units: true state = S * 2^su, with |S| < 2^10 to start with
+    int su = col_scale_exp(S, 4);
+    {
+      const float f = __builtin_amdgcn_ldexpf(1.f, -su);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) S[mt][j] *= f;
+    }
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
       consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], sm.v, &sm.v_free, S, su, a, s + (int64_t)c * C, chunk_len(c), h,
