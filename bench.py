@@ -49,13 +49,13 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_027_955_545,
-    "gdn_recurrent_step_kernel": 1_083_192_613,
-    "causal_conv1d_varlen_kernel": 665_982_052,
-    "causal_conv1d_step_kernel": 59_313_677,
-    "gdn_decode_fused_kernel": 1_131_474_927,
-    "attn_prefill_kernel": 1_327_165_005,
-    "attn_decode_kernel": 1_253_252_670,
+    "gdn_chunk_prefill_kernel": 1_026_359_879,
+    "gdn_recurrent_step_kernel": 1_083_232_910,
+    "causal_conv1d_varlen_kernel": 665_980_056,
+    "causal_conv1d_step_kernel": 59_313_862,
+    "gdn_decode_fused_kernel": 1_131_379_608,
+    "attn_prefill_kernel": 1_328_219_994,
+    "attn_decode_kernel": 1_253_248_268,
 }
 
 
