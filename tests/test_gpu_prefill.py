@@ -55,6 +55,33 @@ def test_prefill_weak_decay(dev):
     _check(case, o, st, o_ref, st_ref)
 
 
+@pytest.mark.parametrize("state_scale", ["zero", "tiny", "large", "mixed"])
+def test_prefill_initial_state_magnitudes(dev, state_scale):
+    """Zero, tiny (1e-20), large (1e6) and per-value-column mixed (1e-15 .. 1e15)
+    initial states under weak decay: the kernel holds the state in power-of-two
+    units per value column, which must follow it from any starting magnitude.
+    Outputs and states are compared in units of their value column's state
+    scale where it exceeds 1: the bars' absolute floors are stated for
+    unit-scale data (at 1e6 one bf16 ulp is ~4e3 and one fp32 ulp ~0.06)."""
+    case = prefill_case([200, 70], seed=13, num_slots=3, Hk=2, Hv=4, g_scale=0.05)
+    col = torch.ones(case.state.shape[-1], dtype=torch.float64)
+    if state_scale == "zero":
+        case.state.zero_()
+    elif state_scale == "tiny":
+        case.state.mul_(1e-19)
+    elif state_scale == "large":
+        case.state.mul_(1e7)
+        col.fill_(1e7)
+    else:
+        col = torch.logspace(-15, 15, case.state.shape[-1], dtype=torch.float64)
+        case.state.mul_(col.float())
+    o, st, o_ref, st_ref = _run(case, dev)
+    unit = col.clamp_min(1.0)
+    assert_out_close(o.double() / unit, o_ref.double() / unit)
+    sel = case.idx.long()
+    assert_state_close(st[sel].double() / unit, st_ref[sel].double() / unit)
+
+
 def test_prefill_zero_decay_beta_one(dev):
     """g = 0, beta = 1: pure delta rule, no decay at all."""
     case = prefill_case([256], seed=9, num_slots=1, Hk=1, Hv=2)
