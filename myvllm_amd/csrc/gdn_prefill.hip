@@ -84,7 +84,7 @@ struct PrefillArgs {
 
 // On-chip data.  The state waves work on chunk c while the producers stage
 // chunk c + 1 and solve the diagonal blocks of T' for chunk c + 2:
-//  * per-chunk tiles, double-buffered by chunk parity (44,560 bytes each);
+//  * per-chunk tiles, double-buffered by chunk parity (44,816 bytes each);
 //  * T' of three consecutive chunks, rotating (17,408 bytes each);
 //  * one V tile: the state waves signal when they have read chunk c's
 //    values, and only then is chunk c + 1's written.
@@ -94,9 +94,11 @@ struct ChunkTiles {
   f16_t p[C * LDH];  // P (fp16), lower triangle
   alignas(16) float gam[C];
   alignas(16) float eg[C];    // e^gamma
+  alignas(16) float ieg[C];   // e^-gamma
   alignas(16) float edec[C];  // e^(gamma_L - gamma), 0 past the chunk's last token
   alignas(16) float beta[C];
   float gam_last;
+  int32_t fact;  // every |gamma| < 80: e^(gamma_i - gamma_j) = e^gamma_i e^-gamma_j (both normal)
 };
 
 // T' = (I + A)^-1 diag(beta) as fp16 hi + lo.  Block (0,1) (rows 0..31,
@@ -112,12 +114,14 @@ struct Smem {
   ChunkTiles tiles[2];
   TBuf tb[3];
   bf16_t v[C * LDV];
-  alignas(16) float dvec[2][2][C];  // waves 4, 5: gamma and beta of the chunk they solve
+  alignas(16) float dvec[2][4][C];  // waves 4, 5: gamma, beta, e^gamma, e^-gamma of the chunk they solve
   int32_t kv_ready;  // chunks whose K tile and decay vectors are staged (wave 6 -> 7)
   int32_t v_free;    // state-wave arrivals after reading the V tile (4 per chunk)
   int32_t pro;       // producer arrivals at the prologue barrier
   int32_t seq;
 };
+static_assert(sizeof(ChunkTiles) == 44816 && sizeof(TBuf) == 17408, "tile sizes as documented above");
+static_assert(sizeof(Smem) <= 160 * 1024, "one workgroup's LDS");
 
 GDN_DEVICE f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -509,6 +513,13 @@ GDN_DEVICE f16x8 bf16x8_to_f16x8(bf16x8 x) {
 
 // gamma = in-chunk cumsum of g (one token per lane) and the per-token decay
 // vectors; g and beta of tokens past the chunk end are taken as zero.
+// Whether every lane's |gamma| < 80, so that e^gamma and e^-gamma are both
+// normal floats and e^(gamma_i - gamma_j) = e^gamma_i e^-gamma_j loses nothing
+// (one rounding per factor instead of an exponential per element).  Wave-uniform.
+GDN_DEVICE bool factorable(float gm) {
+  return __builtin_amdgcn_ballot_w64(!(fabsf(gm) < 80.f)) == 0;
+}
+
 GDN_DEVICE float chunk_gamma(const DecayLoad& dl, int L, int lane, float& gl) {
   const float gm = wave_inclusive_scan(lane < L ? dl.g : 0.f);
   gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gm), 63));  // gamma at token L-1
@@ -538,18 +549,33 @@ GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[8]) {
 // T' buffer (16x16 substitution + one MFMA merge), then T'_bb = T_bb diag(beta)
 // written as fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's
 // LDS accesses complete in program order.  gam and beta: the chunk's vectors.
-GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, const f32x16& G, int blk, int lane) {
+GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, const float* eg, const float* ieg,
+                                 bool fact, const f32x16& G, int blk, int lane) {
   const int n = lane & 31, gq = lane >> 5, o = 32 * blk;
   const Scratch A = scratch_of(tb, blk);
-  const float gj = gam[o + n];
+  if (fact) {
+    const float ej = ieg[o + n];
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) {
-    const f32x4 gi = rows4(gam, o, i4, lane);
-    const f32x4 bi = rows4(beta, o, i4, lane);
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const f32x4 ei = rows4(eg, o, i4, lane);
+      const f32x4 bi = rows4(beta, o, i4, lane);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = 8 * i4 + 4 * gq + rr;
-      A.at(i, n) = i > n ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 8 * i4 + 4 * gq + rr;
+        A.at(i, n) = i > n ? bi[rr] * G[4 * i4 + rr] * (ei[rr] * ej) : 0.f;
+      }
+    }
+  } else {
+    const float gj = gam[o + n];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const f32x4 gi = rows4(gam, o, i4, lane);
+      const f32x4 bi = rows4(beta, o, i4, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 8 * i4 + 4 * gq + rr;
+        A.at(i, n) = i > n ? bi[rr] * G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f;
+      }
     }
   }
   invert_diag16(A, lane);
@@ -580,15 +606,31 @@ GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, 
 GDN_DEVICE void b10_block(const ChunkTiles& ct, TBuf& tb, int lane) {
   const int n = lane & 31, gq = lane >> 5;
   const f32x16 G = gram_tile(ct.k, ct.k, 1, 0, lane);
-  const float gj = ct.gam[n];
+  float d[16];  // e^(gamma_i - gamma_j) for this lane's 16 entries
+  if (__builtin_amdgcn_readfirstlane(ct.fact)) {
+    const float ej = ct.ieg[n];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const f32x4 ei = rows4(ct.eg, 32, i4, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) d[4 * i4 + rr] = ei[rr] * ej;
+    }
+  } else {
+    const float gj = ct.gam[n];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const f32x4 gi = rows4(ct.gam, 32, i4, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) d[4 * i4 + rr] = __expf(gi[rr] - gj);
+    }
+  }
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
-    const f32x4 gi = rows4(ct.gam, 32, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; rr += 2) {
       const int i = 8 * i4 + 4 * gq + rr;
       f16_t h0, h1, l0, l1;
-      split_pair(G[4 * i4 + rr] * __expf(gi[rr] - gj), G[4 * i4 + rr + 1] * __expf(gi[rr + 1] - gj), h0, h1, l0, l1);
+      split_pair(G[4 * i4 + rr] * d[4 * i4 + rr], G[4 * i4 + rr + 1] * d[4 * i4 + rr + 1], h0, h1, l0, l1);
       tb.hi[i * LDH + 32 + n] = h0;
       tb.hi[(i + 1) * LDH + 32 + n] = h1;
       tb.lo[i * LDH + 32 + n] = l0;
@@ -637,25 +679,39 @@ GDN_DEVICE void merge_offdiag(TBuf& tb, int lane) {
 
 // (Q K^T) tile (mt, nt) -> P = lower(q_i.k_j e^(g_i - g_j)) as fp16, C layout
 // (element 4 i4 + rr of the tile at row 32mt + 8 i4 + 4g + rr).
-GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkTiles& ct, int mt, int nt, int h, int lane) {
+GDN_DEVICE f16x8 qk_half(const f32x16& G, const ChunkTiles& ct, bool fact, int mt, int nt, int h, int lane) {
   const int n = lane & 31, gq = lane >> 5;
   const int j = 32 * nt + n;
-  const float gj = ct.gam[j];
   f16x8 out;
+  if (fact) {
+    const float ej = ct.ieg[j];
 #pragma unroll
-  for (int i4 = 2 * h; i4 < 2 * h + 2; ++i4) {
-    const f32x4 gi = rows4(ct.gam, 32 * mt, i4, lane);
+    for (int i4 = 2 * h; i4 < 2 * h + 2; ++i4) {
+      const f32x4 ei = rows4(ct.eg, 32 * mt, i4, lane);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
-      out[4 * (i4 - 2 * h) + rr] = (f16_t)(i >= j ? G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+        out[4 * (i4 - 2 * h) + rr] = (f16_t)(i >= j ? G[4 * i4 + rr] * (ei[rr] * ej) : 0.f);
+      }
+    }
+  } else {
+    const float gj = ct.gam[j];
+#pragma unroll
+    for (int i4 = 2 * h; i4 < 2 * h + 2; ++i4) {
+      const f32x4 gi = rows4(ct.gam, 32 * mt, i4, lane);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 32 * mt + 8 * i4 + 4 * gq + rr;
+        out[4 * (i4 - 2 * h) + rr] = (f16_t)(i >= j ? G[4 * i4 + rr] * __expf(gi[rr] - gj) : 0.f);
+      }
     }
   }
   return out;
 }
 GDN_DEVICE void p_tile(ChunkTiles& ct, int mt, int nt, int lane) {
   const f32x16 G = gram_tile(ct.q, ct.k, mt, nt, lane);
-  const f16x8 h0 = qk_half(G, ct, mt, nt, 0, lane), h1 = qk_half(G, ct, mt, nt, 1, lane);
+  const bool fact = __builtin_amdgcn_readfirstlane(ct.fact) != 0;
+  const f16x8 h0 = qk_half(G, ct, fact, mt, nt, 0, lane), h1 = qk_half(G, ct, fact, mt, nt, 1, lane);
   const int n = lane & 31, gq = lane >> 5;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -681,6 +737,9 @@ GDN_DEVICE void stage_decay(ChunkTiles& ct, const DecayLoad& dl, int L, int b_dt
   const float gm = chunk_gamma(dl, L, lane, gl);
   ct.gam[lane] = gm;
   ct.eg[lane] = __expf(gm);
+  ct.ieg[lane] = __expf(-gm);
+  const bool fact = factorable(gm);
+  if (lane == 0) ct.fact = fact;
   ct.edec[lane] = lane < L ? __expf(gl - gm) : 0.f;
   ct.beta[lane] = lane < L ? scalar_raw_f32(dl.b, b_dtype) : 0.f;
   if (lane == 0) ct.gam_last = gl;
@@ -969,17 +1028,23 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   if (pw < 2) {
     float* dgam = sm.dvec[pw][0];
     float* dbeta = sm.dvec[pw][1];
+    float* deg = sm.dvec[pw][2];
+    float* dieg = sm.dvec[pw][3];
     DiagLoad dl;
     // solve this wave's diagonal block of chunk c (its loads are in dl) into
     // T' buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
     auto solve = [&](int c) __attribute__((always_inline)) {
       float gl;
       const int L = chunk_len(c);
-      dgam[lane] = chunk_gamma(dl.d, L, lane, gl);
+      const float gm = chunk_gamma(dl.d, L, lane, gl);
+      dgam[lane] = gm;
+      deg[lane] = __expf(gm);
+      dieg[lane] = __expf(-gm);
+      const bool fact = factorable(gm);
       dbeta[lane] = lane < L ? scalar_raw_f32(dl.d.b, a.b_dtype) : 0.f;
       const f32x16 G = gram_regs(dl.kf);
       if (c + 1 < nc) load_diag(dl, src, c0_of(c + 1), pw, lane);
-      solve_diag_block(sm.tb[c % 3], dgam, dbeta, G, pw, lane);
+      solve_diag_block(sm.tb[c % 3], dgam, dbeta, deg, dieg, fact, G, pw, lane);
     };
     load_diag(dl, src, c0_of(0), pw, lane);
     solve(0);
