@@ -82,6 +82,16 @@ def test_prefill_initial_state_magnitudes(dev, state_scale):
     assert_state_close(st[sel].double() / unit, st_ref[sel].double() / unit)
 
 
+@pytest.mark.parametrize("g_scale", [1.6, 4.0])
+def test_prefill_strong_decay(dev, g_scale):
+    """Log-decays scaled up so that a chunk's cumulative decay passes e^-80
+    (some chunks at 1.6, all at 4): the decay factors then take one exponential
+    per entry instead of the product of per-token exponentials."""
+    case = prefill_case([400, 130, 64], seed=14, num_slots=3, Hk=2, Hv=4, g_scale=g_scale)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
 def test_prefill_zero_decay_beta_one(dev):
     """g = 0, beta = 1: pure delta rule, no decay at all."""
     case = prefill_case([256], seed=9, num_slots=1, Hk=1, Hv=2)
