@@ -907,19 +907,11 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   const int lm = edl > 0.f ? __builtin_amdgcn_frexp_expf(edl) : kNone;
   const int ed = max(max(er + vm - 6, sm + lm + su - 13), er - 100);
   const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
-  const int dsu = su - ed;
-  if (__builtin_amdgcn_ballot_w64(dsu < -100 || dsu > 100) == 0) {
-    const float sdec = __builtin_amdgcn_ldexpf(edl, dsu);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) S[mt][j] *= sdec;
-  } else {  // a factor outside the fp32 range on some column: scale element by element
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) S[mt][j] = __builtin_amdgcn_ldexpf(S[mt][j] * edl, dsu);
-  }
+  // U = K^T (Vd 2^-ed) from zero accumulators, then S' = S e^gamma_L 2^(su - ed) + U
+  // (one fma per element; the MFMAs need not wait for the decay, and the state
+  // is not carried through the accumulator tuples, which cost a register copy
+  // of all 64 values per chunk)
+  f32x16 U[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     float fd[8];
@@ -935,10 +927,26 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(ct.k, LDK, 32 * mt, 16 * ks, lane);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dhi, S[mt]);
+    for (int mt = 0; mt < 4; ++mt) U[mt] = mfma32(akt[mt], dhi, ks == 0 ? zero16() : U[mt]);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma32(akt[mt], dlo, S[mt]);
+    for (int mt = 0; mt < 4; ++mt) U[mt] = mfma32(akt[mt], dlo, U[mt]);
   }
+  const int dsu = su - ed;
+  float sdec = __builtin_amdgcn_ldexpf(edl, dsu);  // 0 when it underflows: the old state is negligible then
+  if (__builtin_amdgcn_ballot_w64(!(sdec <= 3.0e38f)) != 0) {
+    // the factor overflows on some column: scale element by element first
+    // (the empty asm keeps this rare path out of the common one)
+    asm volatile("");
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) S[mt][j] = __builtin_amdgcn_ldexpf(S[mt][j] * edl, dsu);
+    sdec = 1.f;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S[mt][j] = fmaf(S[mt][j], sdec, U[mt][j]);
   su = ed;
 }
 
