@@ -80,8 +80,32 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _sleep_cycles_per_ms() -> float:
+    """Rate of torch.cuda._sleep's cycle counter, measured once with events."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        stream = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 1_000_000
+        torch.cuda._sleep(n)  # warm
+        torch.cuda.synchronize()
+        a.record(stream)
+        torch.cuda._sleep(n)
+        b.record(stream)
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = n / max(a.elapsed_time(b), 1e-3)
+    return _SLEEP_CYCLES_PER_MS
+
+
 def _time_gpu(fn, steps: int, warmup: int):
-    """Run fn() warmup + steps times; return (wall ms/step, mean kernel ms from per-step events)."""
+    """Run fn() warmup + steps times; return (ms/step over the timed steps, mean
+    kernel ms from per-step events).  The stream is held by a short sleep kernel
+    while the timed steps are enqueued, so they run back to back: a launch that
+    takes less time than the host needs to enqueue it would otherwise be timed
+    together with the host's gaps (the sleep ends before the first timed event)."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -89,7 +113,10 @@ def _time_gpu(fn, steps: int, warmup: int):
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    preroll_ms = min(200.0, 5.0 + 0.2 * steps)  # more than the host needs to enqueue the steps
+    cycles = int(preroll_ms * _sleep_cycles_per_ms())
     torch.cuda.synchronize()
+    torch.cuda._sleep(cycles)
     t0.record(stream)
     for i in range(steps):
         evs[i][0].record(stream)
