@@ -113,10 +113,11 @@ def _time_gpu(fn, steps: int, warmup: int):
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    preroll_ms = min(200.0, 5.0 + 0.2 * steps)  # more than the host needs to enqueue the steps
-    cycles = int(preroll_ms * _sleep_cycles_per_ms())
+    preroll = hasattr(torch.cuda, "_sleep")  # a private torch helper: without it, no pre-roll
+    cycles = int(min(200.0, 5.0 + 0.2 * steps) * _sleep_cycles_per_ms()) if preroll else 0
     torch.cuda.synchronize()
-    torch.cuda._sleep(cycles)
+    if preroll:
+        torch.cuda._sleep(cycles)  # longer than the host needs to enqueue the steps
     t0.record(stream)
     for i in range(steps):
         evs[i][0].record(stream)
