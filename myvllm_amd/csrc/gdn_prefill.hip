@@ -8,17 +8,17 @@
 // keeps everything on chip; only q/k/v/g/beta are read and o written.
 //
 // The workgroup is split by role, and the two roles are software-pipelined
-// over chunks through a double-buffered LDS chunk slot (2 x 80 KiB):
+// over chunks through double-buffered LDS chunk tiles:
 //  * state waves 0..3 hold the fp32 128x128 state in registers (wave w owns
 //    value columns [32w, 32w+32)) and run the state products of chunk c;
-//  * producer waves 4..7 stage chunk c+1 (K, Q, V, decays) into the other
-//    slot and compute everything that does not depend on the state: the
-//    kk^T and qk^T tiles, T' = (I + A)^-1 diag(beta) and P.  Waves 4 and 5
-//    each solve one 32x32 diagonal block of T' on their own, wave 6 forms
-//    B_10 and a P tile, wave 7 the other P tiles; after one producer barrier
-//    wave 4 forms the off-diagonal block T'_10 = -T'_11 B_10 T'_00.
-// Both roles execute one workgroup barrier per chunk; producers synchronise
-// among themselves through an LDS counter (two rounds per chunk).
+//  * producer waves 4..7 stage the next chunks (K, Q, V, decays) and compute
+//    everything that does not depend on the state: the kk^T and qk^T tiles,
+//    T' = (I + A)^-1 diag(beta) and P.  Waves 4 and 5 each solve one 32x32
+//    diagonal block of T' two chunks ahead, wave 6 stages K and the decays
+//    and forms B_10 and the off-diagonal block T'_10 = -T'_11 B_10 T'_00,
+//    wave 7 stages Q, forms the three P tiles and stages V.
+// Both roles execute one workgroup barrier per chunk; within a chunk the
+// waves hand work to each other through LDS arrival counters.
 //
 // Per chunk of L <= 64 tokens (gamma = in-chunk cumsum of g):
 //   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kk^T, MFMA)
