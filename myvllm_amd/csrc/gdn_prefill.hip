@@ -166,14 +166,13 @@ GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
 }
 
-// Exponent E with max|x| in [2^(E-1), 2^E) over one value column of the
-// wave's `nt` C tiles, kNone when the column is zero.  In the C layout lanes
-// l and l ^ 32 hold the two row halves of column l % 32, so the per-lane
-// maximum (a tree of a few dependent operations) needs one exchange between
-// the wave halves; no wave-wide reduction.  Non-negative floats order like
-// their bit patterns, so the exchange takes the maximum on integers.
-constexpr int kNone = -4096;
-GDN_DEVICE int col_max_exp(const f32x16* t, int nt) {
+// Maximum of |x| over one value column of the wave's `nt` C tiles.  In the
+// C layout lanes l and l ^ 32 hold the two row halves of column l % 32, so
+// the per-lane maximum (a tree of a few dependent operations) needs one
+// exchange between the wave halves; no wave-wide reduction.  Non-negative
+// floats order like their bit patterns, so the exchange takes the maximum on
+// integers.
+GDN_DEVICE float col_max(const f32x16* t, int nt) {
   float m[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -186,7 +185,14 @@ GDN_DEVICE int col_max_exp(const f32x16* t, int nt) {
     for (int j = 0; j < w; ++j) m[j] = fmaxf(m[j], m[j + w]);
   const uint32_t v = __builtin_bit_cast(uint32_t, m[0]);
   const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  const float mx = __builtin_bit_cast(float, max(sw[0], sw[1]));
+  return __builtin_bit_cast(float, max(sw[0], sw[1]));
+}
+
+// Exponent E with max|x| in [2^(E-1), 2^E) over one value column, kNone
+// when the column is zero.
+constexpr int kNone = -4096;
+GDN_DEVICE int col_max_exp(const f32x16* t, int nt) {
+  const float mx = col_max(t, nt);
   return mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : kNone;
 }
 
@@ -764,7 +770,8 @@ GDN_DEVICE int out_slot(int s, int m) {
 // picks the new units from the exponents of V' and of the decayed state, so
 // S stays below 2^14 and is split without another pass over it.
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, int32_t* v_free, f32x16 (&S)[4],
-                              int& su, const PrefillArgs& a, int64_t c0, int L, int h, int wave, int lane) {
+                              int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h, int wave,
+                              int lane) {
   // Lane-dependent addresses are cheap to recompute; keeping them out of
   // loop-invariant code motion keeps them out of registers across chunks.
   asm volatile("" : "+v"(lane));
@@ -790,8 +797,8 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
     X[1] = mfma32(ak1, slo, X[1]);
   }
   const int ex = su;
-  // exponent of this column's state maximum (max |S| < 2^sm), for the next units
-  const int sm = col_max_exp(S, 4);
+  // exponent of a bound of this column's state maximum (max |S| <= sb < 2^sm), for the next units
+  const int sm = sb > 0.f ? __builtin_amdgcn_frexp_expf(sb) : kNone;
   // R = V - diag(e^gamma) X in true units (V read transposed: rows are tokens)
   const float xu = __builtin_amdgcn_ldexpf(1.f, ex);
 #pragma unroll
@@ -933,6 +940,9 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   }
   const int dsu = su - ed;
   float sdec = __builtin_amdgcn_ldexpf(edl, dsu);  // 0 when it underflows: the old state is negligible then
+  // bound of the new column maximum: the decayed bound plus the update's (|U| < 2^(vm + er - ed + 6))
+  const float ub = vm == kNone ? 0.f : __builtin_amdgcn_ldexpf(1.f, vm + er - ed + 6);
+  float sbd = sb * sdec;
   if (__builtin_amdgcn_ballot_w64(!(sdec <= 3.0e38f)) != 0) {
     // the factor overflows on some column: scale element by element first
     // (the empty asm keeps this rare path out of the common one)
@@ -942,7 +952,9 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] = __builtin_amdgcn_ldexpf(S[mt][j] * edl, dsu);
     sdec = 1.f;
+    sbd = __builtin_amdgcn_ldexpf(sb * edl, dsu);
   }
+  sb = sbd + ub;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -999,7 +1011,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
 #pragma unroll
       for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
     // state units: true state = S * 2^su, with |S| < 2^10 to start with
-    int su = col_scale_exp(S, 4);
+    const int sme = col_max_exp(S, 4);
+    int su = sme == kNone ? 0 : sme - 10;
+    float sb = sme == kNone ? 0.f : 1024.f;  // upper bound of the column's max |S|, carried across chunks
     {
       const float f = __builtin_amdgcn_ldexpf(1.f, -su);
 #pragma unroll
@@ -1009,8 +1023,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     }
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
-      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], sm.v, &sm.v_free, S, su, a, s + (int64_t)c * C, chunk_len(c), h,
-                    wave, lane);
+      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], sm.v, &sm.v_free, S, su, sb, a, s + (int64_t)c * C, chunk_len(c),
+                    h, wave, lane);
+      // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
+      if ((c & 15) == 15) sb = col_max(S, 4);
       __syncthreads();  // chunk c + 1 is prepared
     }
 #pragma unroll

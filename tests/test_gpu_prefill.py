@@ -92,6 +92,15 @@ def test_prefill_strong_decay(dev, g_scale):
     _check(case, o, st, o_ref, st_ref)
 
 
+def test_prefill_long_no_decay(dev):
+    """4,096 tokens (64 chunks) with g = 0: the state never decays, so its
+    per-column units and magnitude bound are carried through every chunk."""
+    case = prefill_case([4096], seed=15, num_slots=1, Hk=1, Hv=2)
+    case.g.zero_()
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
 def test_prefill_zero_decay_beta_one(dev):
     """g = 0, beta = 1: pure delta rule, no decay at all."""
     case = prefill_case([256], seed=9, num_slots=1, Hk=1, Hv=2)
