@@ -49,13 +49,13 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels; a kernel without an
 # entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_026_278_677,
-    "gdn_recurrent_step_kernel": 1_083_181_993,
-    "causal_conv1d_varlen_kernel": 665_972_996,
-    "causal_conv1d_step_kernel": 59_313_184,
-    "gdn_decode_fused_kernel": 1_131_430_370,
-    "attn_prefill_kernel": 1_326_735_550,
-    "attn_decode_kernel": 1_253_243_076,
+    "gdn_chunk_prefill_kernel": 1_026_275_700,
+    "gdn_recurrent_step_kernel": 1_083_199_150,
+    "causal_conv1d_varlen_kernel": 665_974_958,
+    "causal_conv1d_step_kernel": 59_313_861,
+    "gdn_decode_fused_kernel": 1_131_364_391,
+    "attn_prefill_kernel": 1_327_211_637,
+    "attn_decode_kernel": 1_253_245_959,
 }
 
 
