@@ -7,7 +7,8 @@ This package restates, in plain torch on the CPU, the math of the reference
 * the chunked gated-delta-rule prefill (``ops/gated_delta_rule/gated_delta_rule.py``
   and the six stages it calls),
 * the varlen causal conv1d prefill and the decode conv update (``ops/causal_conv1d.py``),
-* the glue of the GDN layer (``layers/linear_attention.py``, ``layers/norm.py``).
+* the glue of the GDN layer (``layers/linear_attention.py``, ``layers/norm.py``),
+* the full-attention ops beside it (``ops/full_attention.py``; ``attention.py``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it, and only as the checker or the timed CPU baseline.
@@ -26,6 +27,8 @@ Parity pinning (every function is pinned; none is "parity unpinned"):
   brute-force scalar loop and ``torch.nn.functional.conv1d``; update == 1-token
   prefill; new state == last W-1 rows.
 * ``layer`` glue -- closed forms of sigmoid/softplus/L2/RMS norms.
+* ``attention`` -- scalar loops with GQA, closed forms and permuted pages
+  (its module docstring).
 
 The reference itself has no tests, golden vectors or CPU path, and its Triton
 kernels cannot run without a GPU; it is read, never imported or run.

@@ -20,6 +20,16 @@ defects -- K/V read from token 0 of the batch instead of the sequence start
   softmax of the unmasked keys.
 
 Computed here in fp64 without the rounding of P; results are returned in fp64.
+
+Test infrastructure only (imported by ``tests/`` and the CPU baseline of
+``bench.py``).  Pinning, in ``tests/test_oracle.py``: ``flash_attention_prefill_ref``
+equals ``attention_loop_ref`` (scalar loops over heads, queries and keys) for
+GQA, causal and not; closed forms (all-equal scores give the running mean of
+v, the first token returns its own value); ``paged_attention_ref`` over pages
+in permuted order equals the contiguous loop at the positions
+``context_len - len + i``; the committed fixtures ``tests/golden/attn_*``
+reproduce.  ``attention_loop_ref`` itself is the textbook definition written
+as loops.
 """
 from __future__ import annotations
 
