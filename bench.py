@@ -570,7 +570,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN path is benchmarked on a single MI355X "
-              "(the kernels shard over heads/sequences with no communication; see the design notes). "
+              "(the kernels shard over heads and sequences with no communication inside the ops, so each "
+              "GPU would run them on its share). "
               "Run it with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -2,7 +2,7 @@
 
 Replaces ``LinearAttentionCache`` (``cache/linear_attention_cache.py:7-88`` of
 yuyifanbupt/myvllm) with the same constructor arguments, slot allocator and
-zero-on-free semantics, and the survey's corrections:
+zero-on-free semantics, and these corrections:
 
 * the recurrent (SSM) cache holds ``num_v_heads`` heads, the heads the
   kernels index (the reference sizes it with ``num_k_heads``, ``:37-45``);
