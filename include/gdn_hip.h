@@ -112,6 +112,17 @@ int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tenso
  *   out    : (T, Hv, V)  bf16, last stride 1
  * chunk_size must be 64; K = V = 128.  Tokens not covered by any sequence
  * keep whatever `out` held.
+ * Range: the MFMA operands are fp16, so every q and k row must have an L2
+ * norm of at most 128 (the layer's rows are L2-normalised, norm 1) and |v|
+ * entries must stay below 65504; the state may have any magnitude (it is
+ * held in per-column power-of-two units).  Keys of any norm in that range
+ * keep the fp32 state bound (the state-update split is sized from each
+ * chunk's largest key norm).
+ * Failure: the kernel's wave roles hand work to each other through bounded
+ * waits; a wait that gives up (a pipeline error, never expected) writes NaN
+ * to all output rows of that (sequence, v-head) and leaves its state slot
+ * untouched.  GDN_PREFILL_SPIN_LIMIT in the environment overrides the bound
+ * (tests force the give-up path with 0).
  */
 int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                       const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,

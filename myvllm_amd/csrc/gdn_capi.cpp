@@ -7,6 +7,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <stdint.h>
 
 #include "../../include/gdn_hip.h"
@@ -17,7 +18,7 @@ hipError_t gdn_recurrent_step_launch(const gdn_tensor* q, const gdn_tensor* k, c
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    hipStream_t st);
+                                    int32_t spin_limit, hipStream_t st);
 hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
                                        int64_t norm_ch, hipStream_t st);
@@ -249,6 +250,19 @@ int check_fused(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, 
 
 int launch_rc(hipError_t e) { return e == hipSuccess ? GDN_OK : (int)e; }
 
+// Bound of the prefill kernel's internal waits between its wave roles (sleep
+// iterations; never reached when the pipeline is correct).  The environment
+// variable GDN_PREFILL_SPIN_LIMIT overrides it so that a test can force the
+// give-up path (NaN output, state untouched) with every wave still exiting.
+int32_t prefill_spin_limit() {
+  constexpr int32_t kDefault = 1 << 22;
+  const char* env = std::getenv("GDN_PREFILL_SPIN_LIMIT");
+  if (!env || !*env) return kDefault;
+  char* end = nullptr;
+  const long v = std::strtol(env, &end, 10);
+  return (end && *end == 0 && v >= 0 && v <= kDefault) ? (int32_t)v : kDefault;
+}
+
 constexpr int64_t kMaxGridYZ = 65535;
 constexpr int32_t kMaxDecodeSplits = 256;
 
@@ -326,7 +340,7 @@ GDN_EXPORT int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const
   if (chunk_size != 64) return GDN_ERR_CHUNK;
   GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, cu_seqlens, true));
   return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale,
-                                            reinterpret_cast<hipStream_t>(stream)));
+                                            prefill_spin_limit(), reinterpret_cast<hipStream_t>(stream)));
 }
 
 GDN_EXPORT int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,

@@ -13,9 +13,9 @@
 //    value columns [32w, 32w+32)) and run the state products of chunk c;
 //  * producer waves 4..7 stage the next chunks (K, Q, V, decays) and compute
 //    everything that does not depend on the state: the kk^T and qk^T tiles,
-//    T' = (I + A)^-1 diag(beta) and P.  Waves 4 and 5 each solve one 32x32
-//    diagonal block of T' two chunks ahead, wave 6 stages K and the decays
-//    and forms B_10 and the off-diagonal block T'_10 = -T'_11 B_10 T'_00,
+//    T = (I + A)^-1 and P.  Waves 4 and 5 each solve one 32x32
+//    diagonal block of T two chunks ahead, wave 6 stages K and the decays
+//    and forms A_10 and the off-diagonal block T_10 = -T_11 A_10 T_00,
 //    wave 7 stages Q, forms the three P tiles and stages V.
 // Both roles execute one workgroup barrier per chunk; within a chunk the
 // waves hand work to each other through LDS arrival counters.
@@ -23,22 +23,22 @@
 // Per chunk of L <= 64 tokens (gamma = in-chunk cumsum of g):
 //   A  = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j))    (kk^T, MFMA)
 //   P  = lower(q_i.k_j e^(gamma_i - gamma_j))                  (qk^T, MFMA)
-//   T' = (I + A)^-1 diag(beta)    (16x16 diagonal blocks by substitution,
+//   T  = (I + A)^-1              (16x16 diagonal blocks by substitution,
 //                                   off-diagonal blocks by MFMA block merges)
-//   R  = V - diag(e^gamma) K S
-//   V' = T' R                      (= u - w S of the reference)
+//   R  = diag(beta) (V - diag(e^gamma) K S)
+//   V' = T R                      (= u - w S of the reference)
 //   O  = scale [diag(e^gamma) Q S + P V']
 //   S  = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
 //
 // The MFMAs run in fp16 (same rate as bf16): q and k are L2-normalised bf16
 // values, which fp16 holds exactly, and every fp32 operand that feeds the
-// carried state (S, R, the decayed V', T', B_10 and the merge product) is
+// carried state (S, R, the decayed V', T, A_10 and the merge product) is
 // split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  R
 // and V' are first scaled by a power of two per value column (max |x| in
 // [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
 // undone on the fp32 accumulator.  The state is held in power-of-two units
 // per value column that keep |S| < 2^14, so it is split as it stands.  The
-// T' blocks and B_10 (|B_10| <= 1) are split unscaled.  Products that only
+// T blocks (unit diagonal) and A_10 are split unscaled.  Products that only
 // feed o use the hi part.
 //
 // MFMA operand layouts (lane l, n = l % 32, g = l / 32), 32x32x16:
@@ -61,7 +61,6 @@ constexpr int LDK = 136;   // fp16 row stride of the K/Q tiles
 constexpr int LDV = 144;   // bf16 row stride of the V tile (conflict-free transposed reads)
 constexpr int LDH = 68;    // fp16 row stride of T_hi/T_lo/P
 constexpr int kMaxRankedSeqs = 256;  // longest-first ordering for up to this many sequences
-constexpr int kSpinLimit = 1 << 22;  // bound on a producer barrier wait (never reached when correct)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -79,13 +78,14 @@ struct PrefillArgs {
   int32_t Hv, r;
   int32_t b_dtype;
   float scale;
+  int32_t spin_limit;  // bound of a producer wait (sleep iterations)
   bool idx64, cu64;
 };
 
 // On-chip data.  The state waves work on chunk c while the producers stage
-// chunk c + 1 and solve the diagonal blocks of T' for chunk c + 2:
+// chunk c + 1 and solve the diagonal blocks of T for chunk c + 2:
 //  * per-chunk tiles, double-buffered by chunk parity (44,816 bytes each);
-//  * T' of three consecutive chunks, rotating (17,408 bytes each);
+//  * T of three consecutive chunks, rotating (17,408 bytes each);
 //  * one V tile: the state waves signal when they have read chunk c's
 //    values, and only then is chunk c + 1's written.
 struct ChunkTiles {
@@ -101,9 +101,9 @@ struct ChunkTiles {
   int32_t fact;  // every |gamma| < 80: e^(gamma_i - gamma_j) = e^gamma_i e^-gamma_j (both normal)
 };
 
-// T' = (I + A)^-1 diag(beta) as fp16 hi + lo.  Block (0,1) (rows 0..31,
+// T = (I + A)^-1 as fp16 hi + lo.  Block (0,1) (rows 0..31,
 // columns 32..63) is zero and never read by the state waves; the producers
-// keep B_10 there, and while the diagonal blocks are being solved the two
+// keep A_10 there, and while the diagonal blocks are being solved the two
 // off-diagonal blocks hold the fp32 working copies of the diagonal blocks.
 struct TBuf {
   f16_t hi[C * LDH];
@@ -115,9 +115,11 @@ struct Smem {
   TBuf tb[3];
   bf16_t v[C * LDV];
   alignas(16) float dvec[2][4][C];  // waves 4, 5: gamma, beta, e^gamma, e^-gamma of the chunk they solve
+  float kn2[3][2];   // max_t |k_t|^2 over each diagonal block's rows, per T buffer
   int32_t kv_ready;  // chunks whose K tile and decay vectors are staged (wave 6 -> 7)
   int32_t v_free;    // state-wave arrivals after reading the V tile (4 per chunk)
   int32_t pro;       // producer arrivals at the prologue barrier
+  int32_t failed;    // a producer wait gave up (a pipeline logic error): the item's output is NaN
   int32_t seq;
 };
 static_assert(sizeof(ChunkTiles) == 44816 && sizeof(TBuf) == 17408, "tile sizes as documented above");
@@ -215,6 +217,18 @@ GDN_DEVICE float wave_inclusive_scan(float x) {
   return x;
 }
 
+// Maximum over the 64 lanes of a non-negative float (bit patterns order like the values).
+GDN_DEVICE float wave_max(float x) {
+  int v = __builtin_bit_cast(int, x);
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false));  // row_shr:1
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false));  // row_shr:2
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false));  // row_shr:4
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false));  // row_shr:8
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 63));
+}
+
 // hi/lo fp16 splits: hi = fp16(x) (round to nearest even), lo = fp16(x - hi).
 // hi is converted once and its bits are pinned through an empty asm, so the
 // x - hi below is taken from exactly the bits that are stored as hi.  (If the
@@ -300,17 +314,20 @@ GDN_DEVICE void split_vec(const float* x, f16_t* hi, f16_t* lo) {
   for (int m = 0; m < N; m += 2) split_pair(x[m], x[m + 1], hi[m], hi[m + 1], lo[m], lo[m + 1]);
 }
 
-// ---- T' = (I + A)^-1 diag(beta) pieces -------------------------------------------
+// ---- T = (I + A)^-1 pieces ---------------------------------------------------------
 //
-// With B = strict_lower(k_i.k_j e^(gamma_i - gamma_j)) and A = diag(beta) B,
-// T' = (I + diag(beta) B)^-1 diag(beta) is block lower triangular over the two
-// 32-token halves, and its off-diagonal block satisfies
-//   T'_10 = -T'_11 B_10 T'_00,
+// With A = strict_lower(beta_i k_i.k_j e^(gamma_i - gamma_j)), T = (I + A)^-1 is
+// unit lower triangular and block lower triangular over the two 32-token
+// halves, and its off-diagonal block satisfies
+//   T_10 = -T_11 A_10 T_00,
 // so each diagonal block is solved on its own (one wave each) and the
-// off-diagonal block needs only the fp16 hi/lo of T'_00, T'_11 and B_10.
+// off-diagonal block needs only the fp16 hi/lo of T_00, T_11 and A_10.  (beta
+// scales the rows of R instead of the columns of T: with T' = T diag(beta)
+// a small beta pushed T' into fp16's subnormal range, where its split lost
+// precision.)
 
 // fp32 working copy of a 32x32 diagonal block, kept in the two fp16 arrays
-// of an off-diagonal block of the same T' buffer: row i's columns 0..15 in
+// of an off-diagonal block of the same T buffer: row i's columns 0..15 in
 // the hi array, 16..31 in the lo array (64 bytes each, 8-byte aligned).
 struct Scratch {
   // byte address of the block's row 0 in the hi array; the lo array follows
@@ -391,11 +408,11 @@ GDN_DEVICE void merge16(const Scratch& A, int lane) {
 }
 
 // Sequence of rank `rank` in longest-first order (ties by index); called by
-// every thread of the block (the lengths are staged in T' buffer 2, which is
+// every thread of the block (the lengths are staged in T buffer 2, which is
 // first written for chunk 2).
 GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int tid) {
   if (a.nseq > kMaxRankedSeqs) return rank;
-  static_assert(kMaxRankedSeqs * sizeof(int32_t) <= sizeof(TBuf), "lengths fit a T' buffer");
+  static_assert(kMaxRankedSeqs * sizeof(int32_t) <= sizeof(TBuf), "lengths fit a T buffer");
   int32_t* lens = reinterpret_cast<int32_t*>(sm.tb[2].hi);
   for (int64_t i = tid; i < a.nseq; i += kThreads) {
     int64_t s, e;
@@ -422,16 +439,25 @@ GDN_DEVICE int64_t seq_of_rank(Smem& sm, const PrefillArgs& a, int64_t rank, int
 // Producer barriers: LDS arrival counters that grow by the number of
 // arriving waves per chunk.  A wave may arrive without waiting (its data is
 // published by the release fence); waits are bounded so a logic error cannot
-// hang the GPU.
+// hang the GPU.  A wait that gives up raises the workgroup's `failed` flag:
+// the item then writes NaN to its output rows and leaves its state slot
+// untouched, so a pipeline error fails loudly instead of giving a plausible
+// answer.  (spin_limit is a kernel argument so that a test can force the
+// give-up path from the host with every wave still exiting normally.)
 GDN_DEVICE void producer_arrive(int32_t* count, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-GDN_DEVICE void producer_wait(int32_t* count, int32_t target) {
-  for (int spin = 0; spin < kSpinLimit; ++spin) {
-    if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+GDN_DEVICE void producer_wait(int32_t* count, int32_t target, int32_t spin_limit, int32_t* failed) {
+  bool seen = false;
+  for (int spin = 0; spin < spin_limit; ++spin) {
+    if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+      seen = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
+  if (!seen) __hip_atomic_store(failed, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
@@ -453,8 +479,9 @@ GDN_DEVICE int chunk_rows(const ChunkSource& src, int64_t c0) {
 // Rows past the chunk's last token are loaded from the last token instead
 // (no divergent loads, so nothing waits on them early): they are inert
 // because their g, beta and e^(gamma_L - gamma) are set to zero, which zeroes
-// their rows and columns of T' and their share of the state update, and
-// their output rows are not stored.
+// their rows of R and their rows and columns of A (T keeps a unit row and
+// column for them) and their share of the state update, and their output rows
+// are not stored.
 //
 // 16 bytes of row `row` of a chunk (uniform base pointer of the chunk's first
 // token + a 32-bit lane offset; the host guarantees 64 token strides fit).
@@ -550,10 +577,10 @@ GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[8]) {
   return G;
 }
 
-// Diagonal block `blk` of T': A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
+// Diagonal block `blk` of T: A_bb = strict_lower(beta_i k_i.k_j e^(g_i - g_j))
 // from its kk^T tile, solved in fp32 in the off-diagonal block of the same
-// T' buffer (16x16 substitution + one MFMA merge), then T'_bb = T_bb diag(beta)
-// written as fp16 hi/lo.  One wave, no workgroup synchronisation: the wave's
+// T buffer (16x16 substitution + one MFMA merge), then T_bb written as fp16
+// hi/lo.  One wave, no workgroup synchronisation: the wave's
 // LDS accesses complete in program order.  gam and beta: the chunk's vectors.
 GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, const float* eg, const float* ieg,
                                  bool fact, const f32x16& G, int blk, int lane) {
@@ -586,15 +613,14 @@ GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, 
   }
   invert_diag16(A, lane);
   merge16(A, lane);
-  // T'_bb = T_bb diag(beta): lane -> row lane / 2, 16 columns
+  // T_bb (unit diagonal) as fp16 hi/lo: lane -> row lane / 2, 16 columns
   const int i = lane >> 1, half = lane & 1, j0 = 16 * half;
   float tv[16];
 #pragma unroll
   for (int m = 0; m < 16; m += 4) {
     const f32x4 x = load4(A.row(i, half) + m);
-    const f32x4 bb = *reinterpret_cast<const f32x4*>(beta + o + j0 + m);
 #pragma unroll
-    for (int z = 0; z < 4; ++z) tv[m + z] = x[z] * bb[z];
+    for (int z = 0; z < 4; ++z) tv[m + z] = x[z];
   }
   f16_t th[16], tl[16];
   split_vec<16>(tv, th, tl);
@@ -606,9 +632,10 @@ GDN_DEVICE void solve_diag_block(TBuf& tb, const float* gam, const float* beta, 
   }
 }
 
-// B_10 = k_i.k_j e^(g_i - g_j) for tokens i in 32..63, j in 0..31 (always
-// i > j), as fp16 hi/lo in block (0,1) of the T' arrays: B_10[i][j] at row i,
-// column 32 + j.  |B_10| <= 1, so the split needs no scaling.
+// A_10 = beta_i k_i.k_j e^(g_i - g_j) for tokens i in 32..63, j in 0..31
+// (always i > j), as fp16 hi/lo in block (0,1) of the T arrays: A_10[i][j] at
+// row i, column 32 + j.  |A_10| <= beta_i |k_i| |k_j| (<= 1 for unit keys and
+// beta <= 1), split unscaled.
 GDN_DEVICE void b10_block(const ChunkTiles& ct, TBuf& tb, int lane) {
   const int n = lane & 31, gq = lane >> 5;
   const f32x16 G = gram_tile(ct.k, ct.k, 1, 0, lane);
@@ -632,11 +659,13 @@ GDN_DEVICE void b10_block(const ChunkTiles& ct, TBuf& tb, int lane) {
   }
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
+    const f32x4 bi = rows4(ct.beta, 32, i4, lane);
 #pragma unroll
     for (int rr = 0; rr < 4; rr += 2) {
       const int i = 8 * i4 + 4 * gq + rr;
       f16_t h0, h1, l0, l1;
-      split_pair(G[4 * i4 + rr] * d[4 * i4 + rr], G[4 * i4 + rr + 1] * d[4 * i4 + rr + 1], h0, h1, l0, l1);
+      split_pair(G[4 * i4 + rr] * (d[4 * i4 + rr] * bi[rr]), G[4 * i4 + rr + 1] * (d[4 * i4 + rr + 1] * bi[rr + 1]),
+                 h0, h1, l0, l1);
       tb.hi[i * LDH + 32 + n] = h0;
       tb.hi[(i + 1) * LDH + 32 + n] = h1;
       tb.lo[i * LDH + 32 + n] = l0;
@@ -645,12 +674,12 @@ GDN_DEVICE void b10_block(const ChunkTiles& ct, TBuf& tb, int lane) {
   }
 }
 
-// T'_10 = -T'_11 B_10 T'_00 from the fp16 hi/lo blocks (lo x lo dropped).  One wave.
+// T_10 = -T_11 A_10 T_00 from the fp16 hi/lo blocks (lo x lo dropped).  One wave.
 GDN_DEVICE void merge_offdiag(TBuf& tb, int lane) {
   const int n = lane & 31, gq = lane >> 5;
   const f16_t* th = tb.hi;
   const f16_t* tl = tb.lo;
-  // M = B_10 T'_00: A operand = rows of B_10, B operand = columns of T'_00
+  // M = A_10 T_00: A operand = rows of A_10, B operand = columns of T_00
   f32x16 M = zero16();
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -660,7 +689,7 @@ GDN_DEVICE void merge_offdiag(TBuf& tb, int lane) {
     M = mfma32(bh, cl, M);
     M = mfma32(bl, ch, M);
   }
-  // -T'_11 M: A operand = rows of T'_11, B operand = M (C layout rows == k)
+  // -T_11 M: A operand = rows of T_11, B operand = M (C layout rows == k)
   f32x16 R = zero16();
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -769,9 +798,9 @@ GDN_DEVICE int out_slot(int s, int m) {
 // mixes value columns): the update rescales S by one factor per chunk and
 // picks the new units from the exponents of V' and of the decayed state, so
 // S stays below 2^14 and is split without another pass over it.
-GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, int32_t* v_free, f32x16 (&S)[4],
-                              int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h, int wave,
-                              int lane) {
+GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, bf16_t* vt, int32_t* v_free,
+                              f32x16 (&S)[4], int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h,
+                              int wave, int lane) {
   // Lane-dependent addresses are cheap to recompute; keeping them out of
   // loop-invariant code motion keeps them out of registers across chunks.
   asm volatile("" : "+v"(lane));
@@ -799,25 +828,29 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   const int ex = su;
   // exponent of a bound of this column's state maximum (max |S| <= sb < 2^sm), for the next units
   const int sm = sb > 0.f ? __builtin_amdgcn_frexp_expf(sb) : kNone;
-  // R = V - diag(e^gamma) X in true units (V read transposed: rows are tokens)
+  // R = diag(beta) (V - diag(e^gamma) X) in true units (V read transposed:
+  // rows are tokens); beta multiplies R rather than T, so T keeps its unit
+  // diagonal and its fp16 split keeps full precision for any beta
   const float xu = __builtin_amdgcn_ldexpf(1.f, ex);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const f32x4 egv = rows4(ct.eg, 32 * mt, i, lane);
+      const f32x4 bv = rows4(ct.beta, 32 * mt, i, lane);
       const int j = lane & 15, qd = lane >> 4;
       const bf16_t* p = vt + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
       const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu), X[mt][4 * i + rr], (float)vv[rr]);
+      for (int rr = 0; rr < 4; ++rr)
+        X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu * bv[rr]), X[mt][4 * i + rr], (float)vv[rr] * bv[rr]);
     }
   }
   f32x16* R = X;  // X now holds R
   // (er >= ex - 100 keeps 2^(ex - er) finite; a smaller R is negligible next to the state)
   const int er = max(col_scale_exp(R, 2), ex - 100);
   const float rs = __builtin_amdgcn_ldexpf(1.f, -er);
-  // V' = T' R, in units of 2^er (T' lower triangular: rows 0..31 need only k-steps 0, 1)
+  // V' = T R, in units of 2^er (T lower triangular: rows 0..31 need only k-steps 0, 1)
   f32x16 VN[2] = {zero16(), zero16()};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -901,18 +934,21 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   // with the new state in units of 2^ed:  S' = S e^gamma_L 2^(su - ed) + K^T (Vd 2^-ed).
   // ed keeps the split of S' (next chunk, unscaled) inside the fp16 range:
   //  * the update: with max |VN| < 2^vm and edec <= 1 the split operand
-  //    Vd 2^-ed is below 2^(vm + er - ed) <= 2^6 when ed >= er + vm - 6, so
-  //    the update is below 2^6 sum_t |k_t|: 2^12 for L2-normalised keys
-  //    (|k| <= 1), and below 2^15 for any |k| <= 8;
+  //    Vd 2^-ed is below 2^(vm + er - ed), and entry (i, j) of the update is
+  //    below 2^(vm + er - ed) sum_t |k_t,i| <= 2^(vm + er - ed) kb with
+  //    kb = 64 max_t |k_t| (the chunk's largest key norm, from the Gram
+  //    diagonal), so it is below 2^12 when ed >= er + vm + kbe - 12
+  //    (kb <= 2^kbe; kbe = 6 or 7 for L2-normalised keys);
   //  * the decayed state: with max |S| < 2^sm and e^gamma_L < 2^lm it is below
   //    2^(sm + lm + su - ed) <= 2^13 when ed >= sm + lm + su - 13;
-  // so |S'| < 2^13 + 2^12 (and < 2^15 + 2^13 < 65504 for |k| <= 8).  A part
-  // that is zero (sm, vm or lm = kNone) sets no bound; ed >= er - 100 keeps
-  // 2^(er - ed) finite.
+  // so |S'| < 2^13 + 2^12 for keys of any norm.  A part that is zero (sm, vm,
+  // lm or kbe = kNone) sets no bound; ed >= er - 100 keeps 2^(er - ed) finite.
   const float edl = __expf(ct.gam_last);
   const int vm = col_max_exp(VN, 2);
   const int lm = edl > 0.f ? __builtin_amdgcn_frexp_expf(edl) : kNone;
-  const int ed = max(max(er + vm - 6, sm + lm + su - 13), er - 100);
+  const float kb = 64.f * __builtin_sqrtf(kn2);
+  const int kbe = kb > 0.f ? __builtin_amdgcn_frexp_expf(kb) : kNone;
+  const int ed = max(max(er + vm + kbe - 12, sm + lm + su - 13), er - 100);
   const float fdu = __builtin_amdgcn_ldexpf(1.f, er - ed);
   // U = K^T (Vd 2^-ed) from zero accumulators, then S' = S e^gamma_L 2^(su - ed) + U
   // (one fma per element; the MFMAs need not wait for the decay, and the state
@@ -940,8 +976,8 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, bf16_t* vt, 
   }
   const int dsu = su - ed;
   float sdec = __builtin_amdgcn_ldexpf(edl, dsu);  // 0 when it underflows: the old state is negligible then
-  // bound of the new column maximum: the decayed bound plus the update's (|U| < 2^(vm + er - ed + 6))
-  const float ub = vm == kNone ? 0.f : __builtin_amdgcn_ldexpf(1.f, vm + er - ed + 6);
+  // bound of the new column maximum: the decayed bound plus the update's (|U| < 2^(vm + er - ed) kb)
+  const float ub = vm == kNone ? 0.f : __builtin_amdgcn_ldexpf(kb, vm + er - ed);
   float sbd = sb * sdec;
   if (__builtin_amdgcn_ballot_w64(!(sdec <= 3.0e38f)) != 0) {
     // the factor overflows on some column: scale element by element first
@@ -978,6 +1014,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     sm.kv_ready = 0;
     sm.v_free = 0;
     sm.pro = 0;
+    sm.failed = 0;
   }
   __syncthreads();  // the counters are zero before any wave can arrive
   const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
@@ -1023,11 +1060,24 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     }
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
-      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], sm.v, &sm.v_free, S, su, sb, a, s + (int64_t)c * C, chunk_len(c),
-                    h, wave, lane);
+      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], fmaxf(sm.kn2[c % 3][0], sm.kn2[c % 3][1]), sm.v, &sm.v_free, S,
+                    su, sb, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
       // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
       if ((c & 15) == 15) sb = col_max(S, 4);
       __syncthreads();  // chunk c + 1 is prepared
+    }
+    if (__hip_atomic_load(&sm.failed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
+      // a producer wait gave up: NaN in every output row of this item (this
+      // wave's 32 columns), state slot untouched
+      asm volatile("");
+      const bf16_t nan = (bf16_t)__builtin_nanf("");
+      for (int64_t t = s + (lane >> 2); t < e; t += 16) {
+        bf16x8 z;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) z[m] = nan;
+        *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+      }
+      return;
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -1038,8 +1088,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   }
 
   // ---- producer waves.  While the state waves work on chunk c:
-  //  waves 4 / 5: diagonal block 0 / 1 of T' for chunk c + 2;
-  //  wave 6: K tile and decay vectors of chunk c + 1, then B_10 and T'_10 of
+  //  waves 4 / 5: diagonal block 0 / 1 of T for chunk c + 2;
+  //  wave 6: K tile and decay vectors of chunk c + 1, then A_10 and T_10 of
   //          chunk c + 1 (its diagonal blocks were solved one iteration earlier);
   //  wave 7: Q tile and P tiles of chunk c + 1, then its V tile once the
   //          state waves have released the V tile of chunk c.
@@ -1056,7 +1106,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     float* dieg = sm.dvec[pw][3];
     DiagLoad dl;
     // solve this wave's diagonal block of chunk c (its loads are in dl) into
-    // T' buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
+    // T buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
     auto solve = [&](int c) __attribute__((always_inline)) {
       float gl;
       const int L = chunk_len(c);
@@ -1067,13 +1117,21 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       const bool fact = factorable(gm);
       dbeta[lane] = lane < L ? scalar_raw_f32(dl.d.b, a.b_dtype) : 0.f;
       const f32x16 G = gram_regs(dl.kf);
+      // max_i |k_i|^2 over this block's rows: the largest |k_i.k_j| of the Gram (Cauchy-Schwarz)
+      {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(G[j]));
+        m = wave_max(m);
+        if (lane == 0) sm.kn2[c % 3][pw] = m;
+      }
       if (c + 1 < nc) load_diag(dl, src, c0_of(c + 1), pw, lane);
       solve_diag_block(sm.tb[c % 3], dgam, dbeta, deg, dieg, fact, G, pw, lane);
     };
     load_diag(dl, src, c0_of(0), pw, lane);
     solve(0);
     producer_arrive(&sm.pro, lane);
-    producer_wait(&sm.pro, 4);
+    producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
     if (nc > 1) solve(1);
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
@@ -1102,7 +1160,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     load(0);
     stage(0);
     producer_arrive(&sm.pro, lane);
-    producer_wait(&sm.pro, 4);
+    producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
     offdiag(0);
     if (nc > 1) load(1);
     __syncthreads();
@@ -1123,7 +1181,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       ChunkTiles& ct = sm.tiles[c & 1];
       stage_f16(ct.q, ql, lane);
       if (c + 1 < nc) qload(c + 1);
-      producer_wait(&sm.kv_ready, c + 1);
+      producer_wait(&sm.kv_ready, c + 1, a.spin_limit, &sm.failed);
       p_tile(ct, 0, 0, lane);
       p_tile(ct, 1, 0, lane);
       p_tile(ct, 1, 1, lane);
@@ -1134,12 +1192,12 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     stage_v(sm.v, vl, lane);
     if (nc > 1) vload(1);
     producer_arrive(&sm.pro, lane);
-    producer_wait(&sm.pro, 4);
+    producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
     __syncthreads();
     for (int c = 0; c < nc; ++c) {
       if (c + 1 < nc) {
         qp(c + 1);
-        producer_wait(&sm.v_free, 4 * (c + 1));  // the state waves are done with chunk c's V tile
+        producer_wait(&sm.v_free, 4 * (c + 1), a.spin_limit, &sm.failed);  // the state waves are done with chunk c's V tile
         stage_v(sm.v, vl, lane);
         if (c + 2 < nc) vload(c + 2);
       }
@@ -1153,7 +1211,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    hipStream_t st) {
+                                    int32_t spin_limit, hipStream_t st) {
   PrefillArgs a;
   a.q = reinterpret_cast<const bf16_t*>(q->data);
   a.k = reinterpret_cast<const bf16_t*>(k->data);
@@ -1178,6 +1236,7 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   a.r = (int32_t)(v->shape[1] / q->shape[1]);
   a.b_dtype = beta->dtype;
   a.scale = scale;
+  a.spin_limit = spin_limit;
   a.idx64 = idx->dtype == GDN_DTYPE_I64;
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
   const int64_t nwork = a.nseq * a.Hv;

@@ -66,9 +66,14 @@ def gdn_layer_ref(x, w_qkvz, w_ba, conv_weight, A_log, dt_bias, norm_weight, w_o
     """The layer's intended forward (``layers/linear_attention.py:85-122`` with the
     conv on the qkv projection and the norm on o) over a mixed batch: prefill
     tokens first (``cu_seqlens``), then ``num_decode_tokens`` single-token
-    sequences.  The projections' outputs are rounded to x's dtype, as the
-    layer's linear layers return them; everything after is fp64 except the
-    gated norm's fp32.  Mutates both caches; returns (T, hidden) in x's dtype."""
+    sequences.  Values are rounded to x's dtype where the reference layer's
+    ops return that dtype: the projections (``layers/linear.py:29-30``), the
+    conv output (``ops/causal_conv1d.py:241``; here after the per-head L2
+    norm, which the layer applies to it), the GDN output o (``v.dtype``,
+    ``ops/gated_delta_rule/o.py:147``, ``fused_recurrent_gdn.py:116``) and
+    the gated norm's output (``layers/norm.py:58``); everything between is
+    fp64 (the gated norm fp32).  Mutates both caches; returns (T, hidden) in
+    x's dtype."""
     T = x.shape[0]
     Hv, K, V = recurrent_state.shape[1], recurrent_state.shape[2], recurrent_state.shape[3]
     Hk = num_k_heads
@@ -83,14 +88,15 @@ def gdn_layer_ref(x, w_qkvz, w_ba, conv_weight, A_log, dt_bias, norm_weight, w_o
     o = torch.zeros(T, Hv, V, dtype=torch.float64)
     if Tp > 0:
         y = causal_conv1d_fn_ref(qkv[:Tp], conv_weight, conv_state, conv_state_indices[:Np], cu_seqlens)
-        q = l2norm_ref(y[:, : Hk * K].reshape(Tp, Hk, K))
-        k = l2norm_ref(y[:, Hk * K: 2 * Hk * K].reshape(Tp, Hk, K))
-        v = y[:, 2 * Hk * K:].reshape(Tp, Hv, V)
+        q = l2norm_ref(y[:, : Hk * K].reshape(Tp, Hk, K)).to(x.dtype).double()
+        k = l2norm_ref(y[:, Hk * K: 2 * Hk * K].reshape(Tp, Hk, K)).to(x.dtype).double()
+        v = y[:, 2 * Hk * K:].reshape(Tp, Hv, V).to(x.dtype).double()
         g, beta = gdn_gating_ref(a[:Tp], b[:Tp], A_log, dt_bias, dtype=torch.float64)
         o[:Tp] = chunk_gated_delta_rule_ref(q, k, v, g, beta, recurrent_state, recurrent_state_indices[:Np],
                                             cu_seqlens)
     if num_decode_tokens > 0:
         o[Tp:] = gdn_decode_step_ref(qkv[Tp:], conv_weight, conv_state, conv_state_indices[Np:], a[Tp:], b[Tp:],
                                      A_log, dt_bias, recurrent_state, recurrent_state_indices[Np:], Hk)
-    on = rms_norm_gated_ref(o, z.reshape(T, Hv, V), norm_weight, eps=eps).double()
+    o = o.to(x.dtype)
+    on = rms_norm_gated_ref(o, z.reshape(T, Hv, V).to(x.dtype), norm_weight, eps=eps).double()
     return (on.reshape(T, Hv * V) @ w_out.double().t()).to(x.dtype)

@@ -4,19 +4,25 @@ batches vs the fp64 layer oracle (oracle.layer.gdn_layer_ref).
 
 Tolerances: outputs as for every bf16 output (rtol 2e-2, atol 1e-2).  The
 layer rounds its activations to bf16 between ops (the projections, the conv
-output, o before the norm), as the reference layer does, while the oracle
-keeps fp64 after the projections; the carried states therefore differ by
-about bf16 precision and are checked at rtol 3e-2, atol 1e-3 here (the ops'
-own tests hold them to 1e-3 with exact inputs).
+output, o before the norm), as the reference layer does, while the
+end-to-end oracle keeps fp64 after the projections; the carried states of
+that comparison therefore differ by about bf16 precision and are checked at
+rtol 3e-2, atol 1e-3.  The full-shape test also holds the layer's states to
+the 1e-3 bar against the oracle fed with the very activations the layer
+handed to its GDN ops (its own projection, conv and gates, recomputed on the
+GPU), which removes the rounding difference.
 """
 import pytest
 import torch
 
-from conftest import assert_out_close, assert_state_close
+from conftest import S_ATOL, S_RTOL, assert_out_close, assert_state_close
+from myvllm_amd import causal_conv1d_fn
 from myvllm_amd.cache import LinearAttentionCache
 from myvllm_amd.layer import GatedDeltaNet
+from myvllm_amd.norm import gdn_gating
 from myvllm_amd.workloads import cu_from_lengths
-from oracle.layer import gdn_layer_ref
+from oracle.gdn import chunk_gated_delta_rule_ref
+from oracle.layer import gdn_decode_step_ref, gdn_layer_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +80,70 @@ def test_layer_decode_only_and_prefill_only_calls(dev):
     assert_out_close(out, ref)
     out, ref = _step(layer, cache, torch.randn(2, HID, generator=g).bfloat16(), [], s, 2, ref_conv, ref_rec, dev)
     assert_out_close(out, ref)
+
+
+def test_layer_full_shape_4x2048_prefill_128_decode(dev):
+    """The layer workload at its full shape: hidden 2048, Hk 16 / Hv 32,
+    d 128, 4 x 2048 prefill tokens (fresh sequences) and 128 decode tokens
+    (continuing sequences with random conv and SSM states) in one call,
+    weights ~N(0, 0.02)."""
+    hidden, Hk, Hv, n_pre, len_pre, n_dec = 2048, 16, 32, 4, 2048, 128
+    Tp, T = n_pre * len_pre, n_pre * len_pre + n_dec
+    print(f"layer full shape: hidden {hidden}, Hk {Hk} / Hv {Hv}, {n_pre} x {len_pre} prefill + {n_dec} decode",
+          flush=True)
+    layer = GatedDeltaNet(hidden, Hk, Hv, K, V, device=dev)
+    layer.init_random(std=0.02, seed=5)
+    nslots = n_pre + n_dec + 8
+    cache = LinearAttentionCache(1, nslots, 4, K, V, Hk, Hv, torch.bfloat16, dev, conv_dtype=torch.float32)
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    gen = torch.Generator().manual_seed(6)
+    idx = torch.randperm(nslots, generator=gen)[: n_pre + n_dec].to(torch.int32)
+    dec = idx[n_pre:].long()
+    conv0 = torch.zeros(cache.conv_cache[0].shape)
+    rec0 = torch.zeros(cache.recurrent_cache[0].shape)
+    conv0[dec] = torch.randn((n_dec,) + tuple(conv0.shape[1:]), generator=gen)
+    rec0[dec] = torch.randn((n_dec,) + tuple(rec0.shape[1:]), generator=gen) * 0.1
+    cache.conv_cache[0].copy_(conv0)
+    cache.recurrent_cache[0].copy_(rec0)
+    x = torch.randn(T, hidden, generator=gen).bfloat16()
+    cu = cu_from_lengths([len_pre] * n_pre)
+    xd, cud, idxd = x.to(dev), cu.to(dev), idx.to(dev)
+
+    out = layer(xd, cud, idxd, idxd, num_decode_tokens=n_dec)
+    torch.cuda.synchronize()
+    out, conv_gpu, rec_gpu = out.cpu(), cache.conv_cache[0].cpu(), cache.recurrent_cache[0].cpu()
+
+    # 1) the GDN ops at the 1e-3 state bar, on the activations the layer formed
+    L = layer
+    cz = L.conv_dim + L.v_size
+    with torch.no_grad():
+        proj = xd @ L.in_proj.t()
+        y = causal_conv1d_fn(proj[:Tp, :L.conv_dim], L.conv1d_weight, conv0.to(dev), idxd[:n_pre], cud,
+                             l2norm_channels=2 * L.k_size)
+        g, beta = gdn_gating(proj[:Tp, cz + Hv:], proj[:Tp, cz:cz + Hv], L.A_log, L.dt_bias)
+    y, g, beta, proj = y.cpu(), g.cpu(), beta.cpu(), proj.cpu()
+    rec_ops = rec0.clone()
+    print("layer full shape: op-level oracle", flush=True)
+    chunk_gated_delta_rule_ref(y[:, :L.k_size].view(Tp, Hk, K), y[:, L.k_size:2 * L.k_size].view(Tp, Hk, K),
+                               y[:, 2 * L.k_size:].view(Tp, Hv, V), g, beta, rec_ops, idx[:n_pre], cu)
+    gdn_decode_step_ref(proj[Tp:, :L.conv_dim], L.conv1d_weight.detach().cpu(), conv0.clone(), idx[n_pre:],
+                        proj[Tp:, cz + Hv:], proj[Tp:, cz:cz + Hv], L.A_log.detach().cpu(), L.dt_bias.detach().cpu(),
+                        rec_ops, idx[n_pre:], Hk)
+    used = idx.long()
+    assert_state_close(rec_gpu[used], rec_ops[used])
+    untouched = torch.ones(nslots, dtype=torch.bool)
+    untouched[used] = False
+    assert torch.equal(rec_gpu[untouched], rec0[untouched])
+    assert torch.equal(conv_gpu[untouched], conv0[untouched])
+
+    # 2) end to end against the fp64 layer oracle
+    print("layer full shape: end-to-end oracle", flush=True)
+    conv_ref, rec_ref = conv0.clone(), rec0.clone()
+    ref = gdn_layer_ref(x, *_params(layer), conv_ref, idx, rec_ref, idx, cu, Hk, num_decode_tokens=n_dec)
+    assert_out_close(out, ref)
+    err = (rec_gpu[used].double() - rec_ref[used].double()).abs()
+    worst = (err / (S_ATOL + S_RTOL * rec_ref[used].double().abs())).max().item()
+    print(f"layer full shape: worst state error vs the end-to-end oracle = {worst:.3f} x the 1e-3 bar", flush=True)
+    assert_state_close(rec_gpu[used], rec_ref[used], rtol=3e-2, atol=1e-3)
+    assert torch.allclose(conv_gpu, conv_ref.float(), rtol=1e-2, atol=1e-2)
+

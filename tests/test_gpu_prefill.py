@@ -158,3 +158,66 @@ def test_prefill_32k_full(dev):
     assert case.tokens == 35846
     o, st, o_ref, st_ref = _run(case, dev)
     _check(case, o, st, o_ref, st_ref)
+
+
+@pytest.mark.parametrize("key", ["norm1", "norm8", "norm64", "spiky8"])
+def test_prefill_key_magnitudes(dev, key):
+    """Keys that are not unit vectors: L2 norms 1, 8 and 64 in random
+    directions, and norm-8 keys whose mass sits in one coordinate (|k_i| near
+    8), under weak decay over many chunks.  beta is divided by |k|^2 so the
+    delta rule stays contractive (1 - beta |k|^2 in (0, 1)), as the unit-key
+    recurrence is.  The state then scales like 1 / |k|, so outputs and states
+    are compared after multiplying by |k| (the bars are stated for unit-scale
+    data).  The state-update split is sized from each chunk's largest key
+    norm; before that it assumed |k| <= 1."""
+    case = prefill_case([700, 300, 64], seed=21, num_slots=4, Hk=2, Hv=4, g_scale=0.05)
+    gen = torch.Generator().manual_seed(22)
+    k = torch.nn.functional.normalize(torch.randn(case.k.shape, generator=gen), dim=-1)
+    if key == "spiky8":
+        rho = 8.0
+        k = k * 0.05
+        hot = torch.randint(0, k.shape[-1], k.shape[:2], generator=gen)
+        k.scatter_(-1, hot[..., None], 1.0)
+        k = torch.nn.functional.normalize(k, dim=-1)
+    else:
+        rho = float(key[4:])
+    case.k = (k * rho).to(torch.bfloat16)
+    case.beta = case.beta / case.k.float().pow(2).sum(-1).amax().item()
+    case.state.mul_(1.0 / rho)
+    print(f"prefill keys {key}: max |k| entry {case.k.float().abs().max().item():.2f}", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev)
+    assert_out_close(o.double() * rho, o_ref.double() * rho)
+    sel = case.idx.long()
+    assert_state_close(st[sel].double() * rho, st_ref[sel].double() * rho)
+    untouched = torch.ones(st.shape[0], dtype=torch.bool)
+    untouched[sel] = False
+    assert torch.equal(st[untouched], case.state[untouched])
+
+
+def test_prefill_more_than_256_sequences(dev):
+    """300 sequences of 0..200 tokens (a chunked-prefill scheduler's batch):
+    past 256 sequences the kernel takes them in index order instead of
+    longest first."""
+    gen = torch.Generator().manual_seed(23)
+    lengths = torch.randint(0, 201, (300,), generator=gen).tolist()
+    lengths[7] = 0
+    case = prefill_case(lengths, seed=24, num_slots=320, Hk=2, Hv=4)
+    print(f"prefill 300 sequences, {case.tokens} tokens", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_wait_give_up_poisons_the_item(dev, monkeypatch):
+    """The kernel's waits between its wave roles are bounded; one that gives
+    up must not pass as a plausible answer.  Forced from the host (spin limit
+    0, so every wait gives up at once and every wave still runs to its end):
+    every output row is NaN and no state slot is written.  With the default
+    limit restored the same call is correct again."""
+    case = prefill_case([200, 70], seed=25, num_slots=3, Hk=2, Hv=4)
+    monkeypatch.setenv("GDN_PREFILL_SPIN_LIMIT", "0")
+    o, st, _, _ = _run(case, dev)
+    assert torch.isnan(o.float()).all()
+    assert torch.equal(st, case.state)
+    monkeypatch.delenv("GDN_PREFILL_SPIN_LIMIT")
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
