@@ -5,7 +5,9 @@
  * Every entry point takes device pointers wrapped in plain tensor descriptors
  * (pointer, dtype, shape, element strides), launches on the caller's HIP
  * stream, never allocates, never synchronises the host and keeps no global
- * mutable state.  Return value: 0 on success, > 0 a hipError_t from the
+ * mutable state (one exception: paged_attention_decode_noalloc works in a
+ * static device array shared by its calls on a GPU and caches that array's
+ * address per device).  Return value: 0 on success, > 0 a hipError_t from the
  * launch, < 0 a validation code (nothing was launched).  gdn_strerror() maps
  * any code to text.
  *
@@ -69,6 +71,7 @@ extern "C" {
 #define GDN_ERR_ALIGN (-9)      /* pointer/stride misaligned for 16-byte vector access */
 #define GDN_ERR_CONV_WIDTH (-10) /* conv width outside [2, 6] */
 #define GDN_ERR_RANGE (-11)     /* a size exceeds the kernels' index range */
+#define GDN_ERR_SCRATCH (-12)   /* the call needs more than the library's static scratch holds */
 
 #define GDN_MAX_NDIM 4
 
@@ -259,6 +262,26 @@ int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_he
 int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
                            const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
                            gdn_tensor* workspace, int32_t num_splits, float scale, void* stream);
+
+/*
+ * paged_attention_decode without a workspace argument and without any
+ * allocation: the split partials live in a library-owned static device
+ * array of GDN_DECODE_SCRATCH_FLOATS fp32 values (32 MiB, one copy on every
+ * GPU the library runs on, held until the process ends).  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as paged_attention_decode with the
+ * same num_splits; returns GDN_ERR_SCRATCH (nothing launched) when
+ * paged_attention_decode_workspace_size(B, Hq, D, num_splits) exceeds
+ * GDN_DECODE_SCRATCH_FLOATS.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (two streams, two threads) race and
+ * must be ordered by the caller.  The first call on a device looks the
+ * array's address up (hipGetSymbolAddress) with that device current.
+ */
+#define GDN_DECODE_SCRATCH_FLOATS (8 * 1024 * 1024)
+int paged_attention_decode_noalloc(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                                   const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
+                                   int32_t num_splits, float scale, void* stream);
 
 /* Text for any return code of this library. */
 const char* gdn_strerror(int code);

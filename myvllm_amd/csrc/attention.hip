@@ -17,6 +17,15 @@
 // share the same base, so the result is the same softmax.
 #include "gdn_common.h"
 
+#include <mutex>
+
+// Split partials of paged_attention_decode_noalloc: a file-scope device array
+// (one copy per GPU, for the life of the process) instead of a caller
+// workspace.  Host code never passes `scratch` itself to a kernel (on the host
+// the name stands for a host-side shadow, not a device address): the address
+// is looked up once per device with hipGetSymbolAddress.
+static __device__ __align__(256) float scratch[GDN_DECODE_SCRATCH_FLOATS];
+
 namespace {
 
 template <typename T> struct Mma;
@@ -742,6 +751,37 @@ hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, 
   a.c = scale * kLog2e;
   a.causal = true;
   return launch_prefill<true>(a, q->dtype, (int)q->shape[2], nseq, max_seqlen, st);
+}
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on the device that runs stream st, looked up on
+// that device's first call (with the device made current for the lookup and
+// the caller's current device restored) and cached.
+hipError_t attn_decode_scratch(hipStream_t st, float** ptr) {
+  int dev = 0;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t r = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return e;
+    if (r != hipSuccess) return r;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,

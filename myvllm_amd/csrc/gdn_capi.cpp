@@ -42,6 +42,7 @@ hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, 
 hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
                                     const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
                                     int32_t splits, float scale, hipStream_t st);
+hipError_t attn_decode_scratch(hipStream_t st, float** ptr);
 
 #define GDN_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -319,6 +320,8 @@ GDN_EXPORT const char* gdn_strerror(int code) {
     case GDN_ERR_ALIGN: return "pointer or stride misaligned for 16-byte vector access";
     case GDN_ERR_CONV_WIDTH: return "conv width must be in [2, 6]";
     case GDN_ERR_RANGE: return "size exceeds the kernels' index range";
+    case GDN_ERR_SCRATCH: return "the call needs more split scratch than the library's static array holds "
+                                 "(GDN_DECODE_SCRATCH_FLOATS fp32 values); use fewer splits or the workspace entry";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);
@@ -470,9 +473,11 @@ GDN_EXPORT int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64
   return num_seqs * num_q_heads * (int64_t)num_splits * (head_dim + 4);
 }
 
-GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
-                                      const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
-                                      gdn_tensor* workspace, int32_t num_splits, float scale, void* stream) {
+namespace {
+// Checks shared by the two paged decode entries (everything but the workspace).
+int check_paged_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                       const gdn_tensor* block_tables, const gdn_tensor* context_lens, const gdn_tensor* out,
+                       int32_t num_splits) {
   GDN_TRY(check_desc(q, 3));
   GDN_TRY(check_desc(out, 3));
   const int64_t B = q->shape[0];
@@ -485,6 +490,15 @@ GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_c
   const int64_t es = elem_size(k_cache->dtype);
   if (k_cache->shape[1] * std::max(k_cache->stride[1], v_cache->stride[1]) * es >= (int64_t(1) << 31))
     return GDN_ERR_RANGE;
+  return GDN_OK;
+}
+}  // namespace
+
+GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
+                                      const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
+                                      gdn_tensor* workspace, int32_t num_splits, float scale, void* stream) {
+  GDN_TRY(check_paged_decode(q, k_cache, v_cache, block_tables, context_lens, out, num_splits));
+  const int64_t B = q->shape[0];
   float* ws = nullptr;
   if (num_splits > 1) {
     GDN_TRY(check_desc(workspace, 1));
@@ -494,6 +508,23 @@ GDN_EXPORT int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_c
       return GDN_ERR_SHAPE;
     if (B > 0 && !aligned(workspace, 16)) return GDN_ERR_ALIGN;
     ws = reinterpret_cast<float*>(workspace->data);
+  }
+  return launch_rc(attn_paged_decode_launch(q, k_cache, v_cache, block_tables, context_lens, out, ws, num_splits,
+                                            scale, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int paged_attention_decode_noalloc(const gdn_tensor* q, const gdn_tensor* k_cache,
+                                              const gdn_tensor* v_cache, const gdn_tensor* block_tables,
+                                              const gdn_tensor* context_lens, gdn_tensor* out, int32_t num_splits,
+                                              float scale, void* stream) {
+  GDN_TRY(check_paged_decode(q, k_cache, v_cache, block_tables, context_lens, out, num_splits));
+  const int64_t B = q->shape[0];
+  float* ws = nullptr;
+  if (num_splits > 1 && B > 0) {
+    if (paged_attention_decode_workspace_size(B, q->shape[1], q->shape[2], num_splits) > GDN_DECODE_SCRATCH_FLOATS)
+      return GDN_ERR_SCRATCH;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    GDN_TRY(launch_rc(attn_decode_scratch(st, &ws)));
   }
   return launch_rc(attn_paged_decode_launch(q, k_cache, v_cache, block_tables, context_lens, out, ws, num_splits,
                                             scale, reinterpret_cast<hipStream_t>(stream)));

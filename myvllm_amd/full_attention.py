@@ -115,6 +115,35 @@ def paged_flash_attention_decode(
     return out
 
 
+def paged_flash_attention_decode_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    num_splits: int,
+    out: torch.Tensor,
+) -> torch.Tensor:
+    """:func:`paged_flash_attention_decode` for callers that cannot allocate
+    device memory: ``out`` is required, ``num_splits`` is explicit, and the
+    split partials live in the library's static device array (C entry
+    ``paged_attention_decode_noalloc``; at most ``GDN_DECODE_SCRATCH_FLOATS``
+    fp32 values, else ``GdnError``).  Calls that overlap in time on one GPU
+    share that array and race; order them on one stream."""
+    if k_cache.shape[1] != block_size:
+        raise ValueError(f"block_size {block_size} != k_cache.shape[1] {k_cache.shape[1]}")
+    dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens, out)
+    D = _lib.describe
+    rc = _lib.load().paged_attention_decode_noalloc(
+        D(q), D(k_cache), D(v_cache), D(block_tables), D(context_lens), D(out), int(num_splits), float(scale),
+        _lib.stream_handle(dev),
+    )
+    _lib.check("paged_attention_decode_noalloc", rc)
+    return out
+
+
 def paged_flash_attention_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,

@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "gdn_hip.h")
 
 ERR = {"NULL": -1, "NDIM": -2, "SHAPE": -3, "DTYPE": -4, "STRIDE": -5, "HEADS": -6, "HEAD_DIM": -7, "CHUNK": -8,
-       "ALIGN": -9, "CONV_WIDTH": -10, "RANGE": -11}
+       "ALIGN": -9, "CONV_WIDTH": -10, "RANGE": -11, "SCRATCH": -12}
 
 
 def declared_functions():
@@ -331,3 +331,37 @@ def test_decode_workspace_size():
     lib = _lib.load()
     assert lib.paged_attention_decode_workspace_size(3, 16, 256, 1) == 0
     assert lib.paged_attention_decode_workspace_size(3, 16, 256, 4) == 3 * 16 * 4 * 260
+
+
+def _call_paged_decode_noalloc(a):
+    return _lib.load().paged_attention_decode_noalloc(D(a["q"]), D(a["kc"]), D(a["vc"]), D(a["tab"]), D(a["ctx"]),
+                                                      D(a["out"]), a["splits"], 1.0, None)
+
+
+@cpu_only
+def test_paged_decode_noalloc_validation():
+    a = _paged_attn_args()
+    a.update(kc=torch.zeros(5, 16, 256, dtype=torch.bfloat16))
+    assert _call_paged_decode_noalloc(a) == ERR["NDIM"]
+    a = _paged_attn_args()
+    a.update(splits=257)
+    assert _call_paged_decode_noalloc(a) == ERR["RANGE"]
+    a = _paged_attn_args()
+    a.update(tab=torch.zeros(3, 2, dtype=torch.int32).t())
+    assert _call_paged_decode_noalloc(a) == ERR["STRIDE"]
+
+
+@cpu_only
+def test_paged_decode_noalloc_rejects_more_than_the_static_scratch():
+    # 64 sequences x 64 query heads x 256 splits x (256 + 4) fp32 partials > GDN_DECODE_SCRATCH_FLOATS
+    B, Hq, Hkv, Dh = 64, 64, 8, 256
+    a = dict(q=torch.zeros(B, Hq, Dh, dtype=torch.bfloat16), kc=torch.zeros(4, 16, Hkv, Dh, dtype=torch.bfloat16),
+             vc=torch.zeros(4, 16, Hkv, Dh, dtype=torch.bfloat16), tab=torch.zeros(B, 4, dtype=torch.int32),
+             ctx=torch.ones(B, dtype=torch.int32), out=torch.zeros(B, Hq, Dh, dtype=torch.bfloat16), splits=256)
+    text = open(HEADER).read()
+    cap = eval(re.search(r"#define GDN_DECODE_SCRATCH_FLOATS \(([^)]*)\)", text).group(1))
+    assert _lib.load().paged_attention_decode_workspace_size(B, Hq, Dh, 256) > cap
+    assert _call_paged_decode_noalloc(a) == ERR["SCRATCH"]
+    a["splits"] = 1  # no partials: nothing needs the scratch
+    assert _lib.load().paged_attention_decode_workspace_size(B, Hq, Dh, 1) == 0
+
