@@ -93,7 +93,7 @@ def recurrent_gated_delta_rule_ref(
 def tril_inverse_ref(A: torch.Tensor) -> torch.Tensor:
     """(I + A)^-1 for strictly-lower A (..., C, C).
 
-    Follows the contract of ``ops/gated_delta_rule/solve_tril.py:301-315``
+    Follows the contract of ``ops/gated_delta_rule/solve_tril.py:81-96``
     (docstring) -- computed here by forward substitution row by row, so that
     tests can pin it against ``torch.linalg.solve_triangular``.
     """
@@ -126,14 +126,14 @@ def chunk_gated_delta_rule_ref(
 
     * gamma = in-chunk inclusive cumsum of g (``ops/gated_delta_rule/cumsum.py:37-39``);
     * A = strict-lower[beta_i k_i.k_j exp(gamma_i - gamma_j)]
-      (``ops/gated_delta_rule/chunk_scaled_dot_kkt.py:131-163``);
-    * Tm = (I + A)^-1 (``ops/gated_delta_rule/solve_tril.py:258-293``);
+      (``ops/gated_delta_rule/chunk_scaled_dot_kkt.py:50-84``);
+    * Tm = (I + A)^-1 (``ops/gated_delta_rule/solve_tril.py:6-73``);
     * W = Tm diag(beta e^gamma) K, U = Tm diag(beta) V (``ops/gated_delta_rule/wu.py:90-133``);
-    * V' = U - W S (``ops/gated_delta_rule/h.py:328-344``);
+    * V' = U - W S (``ops/gated_delta_rule/h.py:129-145``);
     * O = scale [diag(e^gamma) Q S + (tril0(Q K^T) * e^(gamma_i - gamma_j)) V']
       (``ops/gated_delta_rule/o.py:81-121``);
-    * S <- e^gamma_last S + K^T diag(e^(gamma_last - gamma)) V' (``ops/gated_delta_rule/h.py:347-373``);
-    * final S written to ``recurrent_state[slot]`` (``ops/gated_delta_rule/h.py:376-391``).
+    * S <- e^gamma_last S + K^T diag(e^(gamma_last - gamma)) V' (``ops/gated_delta_rule/h.py:147-175``);
+    * final S written to ``recurrent_state[slot]`` (``ops/gated_delta_rule/h.py:177-192``).
 
     The initial S is read from ``recurrent_state[slot]``.  All chunks of a
     sequence are formed at once (batched intra-chunk math); only the state
