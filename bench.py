@@ -15,12 +15,17 @@ Hq 16 / Hkv 2, d 256) and paged decode (batch 256, contexts U[512, 4096],
 16-token pages), each with its roofline and, where it applies, the CPU
 oracle timed on this host.  Beside the datasheet peaks, the default run
 measures two ceilings of this device (a bf16 8192^3 GEMM through hipBLASLt and
-a 1 GiB copy) and gives each roofline as a fraction of the matching one too.
+a 1 GiB copy by a plain HIP streaming kernel) and gives each roofline as a
+fraction of the matching one too.
 
 A step is one call of the op on inputs already resident in HBM.  Timing:
 W untimed warm-up steps, then K steps bracketed by device synchronisation;
 per-launch kernel time from HIP events recorded on the stream the kernel is
-launched on.
+launched on, reported as the median over the K launches (``kernel_ms``, the
+figure the rooflines use) with the mean beside it (``kernel_ms_mean``).  The
+CPU baselines run torch on os.cpu_count() threads, or on the CPUs the process
+is confined to where that is fewer (affinity mask, cgroup quota); each
+reports all of these and lscpu's model name.
 """
 from __future__ import annotations
 
@@ -44,10 +49,10 @@ HK, HV, DK, DV, CHUNK = 16, 32, 128, 128, 64
 PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK + 3 * DK * DV) * HV)
 # HBM bytes per launch of each kernel on this benchmark's workloads, from
 # rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch), each
-# scaled by what the same counter reads on a plain 1 GiB device copy
+# scaled by what the same counter reads on a plain 1 GiB streaming copy
 # (--workload hbm_copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0 on MI355X).  Values
-# from the committed profiles of the current kernels; a kernel without an
-# entry reports None.
+# from the committed profiles of the current kernels (profiles/*.md, which
+# give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
     "gdn_chunk_prefill_kernel": 1_026_275_700,
     "gdn_recurrent_step_kernel": 1_083_199_150,
@@ -56,6 +61,7 @@ HBM_TRAFFIC_PER_LAUNCH = {
     "gdn_decode_fused_kernel": 1_131_364_391,
     "attn_prefill_kernel": 1_327_211_637,
     "attn_decode_kernel": 1_253_245_959,
+    "attn_paged_prefill_kernel": 1_153_418_650,
 }
 
 
@@ -63,13 +69,17 @@ def _traffic(kernel: str):
     return HBM_TRAFFIC_PER_LAUNCH.get(kernel)
 
 
-def _cpu_threads() -> int:
-    env = os.environ.get("OMP_NUM_THREADS")
-    n = int(env) if env and env.isdigit() else (os.cpu_count() or 1)
-    return max(1, min(n, 16))
-
-
 def _cpu_model() -> str:
+    """lscpu's model name (/proc/cpuinfo where lscpu is missing)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -78,6 +88,51 @@ def _cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def _cpu_info() -> dict:
+    """The host's CPUs as the CPU baseline sees them: os.cpu_count(), the CPUs
+    this process may run on (affinity mask), the cgroup CPU quota, and the
+    thread count used: os.cpu_count() unless the process is confined to fewer
+    CPUs, where more threads than CPUs would time contention, not the CPU."""
+    info = {"os_cpu_count": os.cpu_count() or 1, "model": _cpu_model()}
+    usable = info["os_cpu_count"]
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+        usable = min(usable, info["affinity_cpus"])
+    except (AttributeError, OSError):
+        info["affinity_cpus"] = None
+    info["cgroup_cpu_quota"] = None
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            info["cgroup_cpu_quota"] = int(quota) / int(period)
+            usable = min(usable, max(1, int(info["cgroup_cpu_quota"])))
+    except (OSError, ValueError):
+        pass
+    info["threads"] = usable
+    return info
+
+
+_CPU_INFO = None
+
+
+def _cpu_setup() -> dict:
+    """Set torch's CPU thread count for a CPU baseline; returns the CPU info."""
+    global _CPU_INFO
+    if _CPU_INFO is None:
+        _CPU_INFO = _cpu_info()
+    torch.set_num_threads(_CPU_INFO["threads"])
+    _CPU_INFO["torch_threads"] = torch.get_num_threads()
+    return _CPU_INFO
+
+
+def _cpu_baseline(value, unit, sample) -> dict:
+    info = _cpu_setup()
+    return {"value": value, "unit": unit, "cores": info["torch_threads"], "kind": "port", "sample": sample,
+            "os_cpu_count": info["os_cpu_count"], "affinity_cpus": info["affinity_cpus"],
+            "cgroup_cpu_quota": info["cgroup_cpu_quota"], "torch_threads": info["torch_threads"],
+            "cpu_model": info["model"]}
 
 
 _SLEEP_CYCLES_PER_MS = None
@@ -100,9 +155,24 @@ def _sleep_cycles_per_ms() -> float:
     return _SLEEP_CYCLES_PER_MS
 
 
-def _time_gpu(fn, steps: int, warmup: int):
-    """Run fn() warmup + steps times; return (ms/step over the timed steps, mean
-    kernel ms from per-step events).  The stream is held by a short sleep kernel
+class Timing:
+    """ms per step over the timed region, and the per-launch kernel time from
+    the per-step events: median (the reported figure) and mean."""
+
+    def __init__(self, step_ms: float, per: list):
+        self.step_ms = step_ms
+        srt = sorted(per)
+        n = len(srt)
+        self.median_ms = srt[n // 2] if n % 2 else 0.5 * (srt[n // 2 - 1] + srt[n // 2])
+        self.mean_ms = sum(per) / n
+
+    def fields(self) -> dict:
+        return {"ms_per_step": self.step_ms, "kernel_ms": self.median_ms, "kernel_ms_mean": self.mean_ms}
+
+
+def _time_gpu(fn, steps: int, warmup: int) -> Timing:
+    """Run fn() warmup + steps times; return the Timing of the timed steps
+    (per-step HIP events on the launch stream).  The stream is held by a short sleep kernel
     while the timed steps are enqueued, so they run back to back: a launch that
     takes less time than the host needs to enqueue it would otherwise be timed
     together with the host's gaps (the sleep ends before the first timed event)."""
@@ -126,8 +196,7 @@ def _time_gpu(fn, steps: int, warmup: int):
     t1.record(stream)
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
-    per = [a.elapsed_time(b) for a, b in evs]
-    return total / steps, sum(per) / len(per)
+    return Timing(total / steps, [a.elapsed_time(b) for a, b in evs])
 
 
 def _time_cpu(fn, budget_s: float, max_reps: int = 5):
@@ -153,13 +222,14 @@ def bench_prefill(dev, steps, warmup, cpu_budget):
     def step(_):
         chunk_gated_delta_rule(q, k, v, g, beta, state, idx, cu)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     flop = PREFILL_FLOP_PER_TOKEN * T
     achieved = flop / (kern_ms * 1e-3) / 1e12
     res = {
         "tokens": T,
         "ms_per_step": ms,
-        "kernel_ms": kern_ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
         "tokens_per_s": T / (ms * 1e-3),
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": _traffic("gdn_chunk_prefill_kernel"),
@@ -168,13 +238,12 @@ def bench_prefill(dev, steps, warmup, cpu_budget):
     if cpu_budget > 0:
         from oracle.gdn import chunk_gated_delta_rule_ref
 
-        torch.set_num_threads(_cpu_threads())
+        _cpu_setup()
         st = case.state.clone()
         sec = _time_cpu(lambda: chunk_gated_delta_rule_ref(case.q, case.k, case.v, case.g, case.beta, st, case.idx,
                                                            case.cu, dtype=torch.float32), cpu_budget)
-        res["cpu_baseline"] = {"value": T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"full workload ({T} tokens), fp32 chunked (C=64) torch restatement, "
-                                         f"{_cpu_model()}"}
+        res["cpu_baseline"] = _cpu_baseline(T / sec, "tokens/s",
+                                            f"full workload ({T} tokens), fp32 chunked (C=64) torch restatement")
     return res
 
 
@@ -194,14 +263,15 @@ def bench_decode(dev, steps, warmup, cpu_budget):
     def step(i):
         recurrent_gated_delta_rule(q, k, v, g, beta, state, idxs[i % 4])
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     per_seq = 2 * HV * DK * DV * 4 + (2 * HK * DK + 2 * HV * DV) * 2 + 2 * HV * 4 + 4
     nbytes = per_seq * B
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     res = {
         "batch": B,
         "ms_per_step": ms,
-        "kernel_ms": kern_ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
         "GB_per_s": gbs,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                      "traffic": _traffic("gdn_recurrent_step_kernel"), "bytes_per_launch": nbytes,
@@ -210,15 +280,15 @@ def bench_decode(dev, steps, warmup, cpu_budget):
     if cpu_budget > 0:
         from oracle.gdn import recurrent_gated_delta_rule_ref
 
-        torch.set_num_threads(_cpu_threads())
+        _cpu_setup()
         sub = 32  # bounded sample: 32 of the 256 sequences (64 MB of state)
         st = torch.randn(sub, HV, DK, DV) * 0.1
         sidx = torch.arange(sub, dtype=torch.int32)
         sec = _time_cpu(lambda: recurrent_gated_delta_rule_ref(case.q[:sub], case.k[:sub], case.v[:sub], case.g[:sub],
                                                                case.beta[:sub], st, sidx, dtype=torch.float32),
                         cpu_budget)
-        res["cpu_baseline"] = {"value": per_seq * sub / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"{sub} of {B} sequences, fp32 token recurrence"}
+        res["cpu_baseline"] = _cpu_baseline(per_seq * sub / sec / 1e9, "GB/s",
+                                            f"{sub} of {B} sequences, fp32 token recurrence")
     return res
 
 
@@ -233,22 +303,22 @@ def bench_conv(dev, steps, warmup, cpu_budget):
     def step(_):
         causal_conv1d_fn(x, w, st, idx, cu)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     nbytes = 4 * T * D + 2 * D * W + 2 * N * (W - 1) * D * 4
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    res = {"tokens": T, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+    res = {"tokens": T, "ms_per_step": ms, "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms, "GB_per_s": gbs,
            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("causal_conv1d_varlen_kernel"),
                         "bytes_per_launch": nbytes, "kernel": "causal_conv1d_varlen_kernel"}}
     if cpu_budget > 0:
         from oracle.conv import causal_conv1d_fn_ref
 
-        torch.set_num_threads(_cpu_threads())
+        _cpu_setup()
         cst = case.state.clone()
         sec = _time_cpu(lambda: causal_conv1d_fn_ref(case.x, case.weight, cst, case.idx, case.cu, dtype=torch.float32),
                         cpu_budget)
-        res["cpu_baseline"] = {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": "full workload, fp32 F.conv1d + SiLU per sequence"}
+        res["cpu_baseline"] = _cpu_baseline(nbytes / sec / 1e9, "GB/s", "full workload, fp32 F.conv1d + SiLU per sequence")
     return res
 
 
@@ -265,10 +335,11 @@ def bench_conv_update(dev, steps, warmup, cpu_budget):
     def step(i):
         causal_conv1d_update(x, w, st, idxs[i % 4])
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     nbytes = 4 * B * D + 2 * D * W + 2 * B * (W - 1) * D * 4
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms, "GB_per_s": gbs,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("causal_conv1d_step_kernel"),
                          "bytes_per_launch": nbytes, "kernel": "causal_conv1d_step_kernel"}}
@@ -295,7 +366,8 @@ def bench_decode_fused(dev, steps, warmup, cpu_budget):
     def step(i):
         gated_delta_net_decode_step(x, w, cs, idxs[i % 4], a, b, A_log, dt_bias, state, idxs[i % 4], HK)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
 
     def separate(i):  # layers/linear_attention.py:89-90, :95, :97-114, :119 as separate ops
         beta = b.sigmoid()
@@ -307,11 +379,11 @@ def bench_decode_fused(dev, steps, warmup, cpu_budget):
         k = k * torch.rsqrt(k.pow(2).sum(dim=-1, keepdim=True) + 1e-6)
         recurrent_gated_delta_rule(q, k, v, g, beta, state, idxs[i % 4])
 
-    ms_sep, _ = _time_gpu(separate, steps, warmup)
+    ms_sep = _time_gpu(separate, steps, warmup).step_ms
     per_seq = 2 * HV * DK * DV * 4 + 2 * (CONV_WIDTH - 1) * D * 4 + D * 2 + HV * DV * 2 + 2 * HV * 2
     nbytes = per_seq * B + D * CONV_WIDTH * 2 + 2 * HV * 4
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+    return {"batch": B, "ms_per_step": ms, "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms, "GB_per_s": gbs,
             "separate_ops_ms_per_step": ms_sep,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("gdn_decode_fused_kernel"),
@@ -340,7 +412,7 @@ def bench_layer(dev, steps, warmup, cpu_budget):
     def step(_):
         layer(x, cu, slots, slots, num_decode_tokens=n_dec)
 
-    ms, _ = _time_gpu(step, steps, warmup)
+    ms = _time_gpu(step, steps, warmup).step_ms
 
     # the same forward, stage by stage, with events between the stages
     Tp, Np, L = n_pre * len_pre, n_pre, layer
@@ -380,7 +452,7 @@ def bench_layer(dev, steps, warmup, cpu_budget):
     gdn_flop = PREFILL_FLOP_PER_TOKEN * Tp
     flop = gemm_flop + gdn_flop
     achieved = flop / (ms * 1e-3) / 1e12
-    return {"tokens": T, "prefill_tokens": Tp, "decode_tokens": n_dec, "ms_per_step": ms, "kernel_ms": ms,
+    return {"tokens": T, "prefill_tokens": Tp, "decode_tokens": n_dec, "ms_per_step": ms, "kernel_ms": ms, "kernel_ms_mean": ms,
             "tokens_per_s": T / (ms * 1e-3),
             "stages_ms": {n: round(v, 4) for n, v in zip(names, acc)},
             "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
@@ -403,7 +475,8 @@ def bench_attn_prefill(dev, steps, warmup, cpu_budget):
         flash_attention_prefill(q, k, v, cu, case.scale, ATTN_HQ, ATTN_HKV, ATTN_D, ATTN_D, True,
                                 max_seqlen=max_len, out=out)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     lens = (case.cu[1:] - case.cu[:-1]).tolist()
     tokens = int(case.cu[-1])
     pairs = sum(n * (n + 1) // 2 for n in lens)  # (query, visible key) pairs
@@ -412,7 +485,7 @@ def bench_attn_prefill(dev, steps, warmup, cpu_budget):
     res = {
         "tokens": tokens,
         "ms_per_step": ms,
-        "kernel_ms": kern_ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
         "tokens_per_s": tokens / (kern_ms * 1e-3),
         "TFLOP_per_s": tflops,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
@@ -422,14 +495,13 @@ def bench_attn_prefill(dev, steps, warmup, cpu_budget):
     if cpu_budget > 0:
         from oracle.attention import attention_rows_ref
 
-        torch.set_num_threads(_cpu_threads())
+        _cpu_setup()
         n0 = lens[2]  # bounded sample: the third sequence (1,405 tokens) in full
         s0 = int(case.cu[2])
         sl = slice(s0, s0 + n0)
         sec = _time_cpu(lambda: attention_rows_ref(case.q[sl], case.k[sl], case.v[sl], torch.arange(n0), case.scale),
                         cpu_budget, max_reps=3)
-        res["cpu_baseline"] = {"value": n0 / sec, "unit": "tokens/s", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"one sequence of {n0} tokens, fp64 causal attention"}
+        res["cpu_baseline"] = _cpu_baseline(n0 / sec, "tokens/s", f"one sequence of {n0} tokens, fp64 causal attention")
     return res
 
 
@@ -449,7 +521,8 @@ def bench_attn_paged_prefill(dev, steps, warmup, cpu_budget):
         paged_flash_attention_prefill(q, kc, vc, tab, ctx, cu, None, case.scale, case.page, max_seqlen=max_len,
                                       out=out)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     lens = (case.cu[1:] - case.cu[:-1]).tolist()
     ctxs = case.context_lens.tolist()
     pairs = sum(n * (L - n) + n * (n + 1) // 2 for n, L in zip(lens, ctxs))  # visible (query, key) pairs
@@ -460,12 +533,12 @@ def bench_attn_paged_prefill(dev, steps, warmup, cpu_budget):
         "tokens": tokens,
         "cached_keys": int(sum(ctxs)),
         "ms_per_step": ms,
-        "kernel_ms": kern_ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
         "tokens_per_s": tokens / (kern_ms * 1e-3),
         "TFLOP_per_s": tflops,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / PEAK_MFMA_TFLOPS, "traffic": None, "flop_per_launch": flops,
-                     "kernel": "attn_prefill_kernel (paged)"},
+                     "frac": tflops / PEAK_MFMA_TFLOPS, "traffic": _traffic("attn_paged_prefill_kernel"),
+                     "flop_per_launch": flops, "kernel": "attn_prefill_kernel (paged)"},
     }
 
 
@@ -486,7 +559,8 @@ def bench_attn_decode(dev, steps, warmup, cpu_budget):
     def step(_):
         paged_flash_attention_decode(q, kc, vc, tab, ctx, case.scale, case.page, num_splits=splits, out=out)
 
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
     keys = int(case.context_lens.sum())
     pages = int(((case.context_lens + case.page - 1) // case.page).sum())
     # K and V rows of every cached key, q and o, the table entries and lengths
@@ -497,7 +571,7 @@ def bench_attn_decode(dev, steps, warmup, cpu_budget):
         "cached_keys": keys,
         "splits": splits,
         "ms_per_step": ms,
-        "kernel_ms": kern_ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
         "GB_per_s": gbs,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                      "traffic": _traffic("attn_decode_kernel"), "bytes_per_launch": nbytes,
@@ -506,7 +580,7 @@ def bench_attn_decode(dev, steps, warmup, cpu_budget):
     if cpu_budget > 0:
         from oracle.attention import attention_rows_ref, gather_paged
 
-        torch.set_num_threads(_cpu_threads())
+        _cpu_setup()
         sub = 16  # bounded sample: 16 of the 256 sequences
 
         def cpu():
@@ -517,44 +591,69 @@ def bench_attn_decode(dev, steps, warmup, cpu_budget):
 
         sec = _time_cpu(cpu, cpu_budget, max_reps=3)
         sub_bytes = int(case.context_lens[:sub].sum()) * ATTN_HKV * ATTN_D * 2 * 2
-        res["cpu_baseline"] = {"value": sub_bytes / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"{sub} of {B} sequences, fp64 attention over gathered pages"}
+        res["cpu_baseline"] = _cpu_baseline(sub_bytes / sec / 1e9, "GB/s",
+                                            f"{sub} of {B} sequences, fp64 attention over gathered pages")
     return res
 
 
-def bench_hbm_copy(dev, steps, warmup, cpu_budget):
-    """Plain 1 GiB device-to-device copy: the calibration point of the HBM
-    byte counters and the copy bandwidth this device reaches."""
+def _hbm_copy_fn(src, dst, blocks):
+    from myvllm_amd import _lib
+
+    lib = _lib.load()
+    stream = _lib.stream_handle(src.device)
+
+    def step(_):
+        _lib.check("gdn_hbm_copy", lib.gdn_hbm_copy(src.data_ptr(), dst.data_ptr(), src.numel(), blocks, stream))
+
+    return step
+
+
+HBM_COPY_BLOCKS = (1024, 2048, 4096, 8192, 0)  # grids the ceiling is taken over (0: one pass, 262,144 workgroups)
+
+
+def bench_hbm_copy(dev, steps, warmup, cpu_budget, blocks=None):
+    """Plain 1 GiB device-to-device copy with the library's HIP streaming
+    kernel (16-byte non-temporal loads and stores): the calibration point of
+    the HBM byte counters and the measured bandwidth ceiling of this device.
+    Without ``blocks`` the best of the grids in HBM_COPY_BLOCKS is reported."""
     n = 1 << 30
     src = torch.empty(n, dtype=torch.uint8, device=dev).random_()
     dst = torch.empty_like(src)
-
-    def step(_):
-        dst.copy_(src)
-
-    ms, kern_ms = _time_gpu(step, steps, warmup)
+    best = None
+    for nb in ((blocks,) if blocks is not None else HBM_COPY_BLOCKS):
+        tm = _time_gpu(_hbm_copy_fn(src, dst, nb), steps, warmup)
+        if best is None or tm.median_ms < best[1].median_ms:
+            best = (nb, tm)
+    assert torch.equal(src[-4096:], dst[-4096:]) and torch.equal(src[:4096], dst[:4096])
+    nb, tm = best
     nbytes = 2 * n
-    gbs = nbytes / (kern_ms * 1e-3) / 1e9
-    return {"bytes": nbytes, "ms_per_step": ms, "kernel_ms": kern_ms, "GB_per_s": gbs,
+    gbs = nbytes / (tm.median_ms * 1e-3) / 1e9
+    return {"bytes": nbytes, "blocks": nb, **tm.fields(), "GB_per_s": gbs,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
-                         "kernel": "torch elementwise copy"}}
+                         "kernel": "hbm_stream_copy_kernel"}}
 
 
 def measure_peaks(dev, steps, warmup):
     """Ceilings measured on this device beside the datasheet peaks: a large
-    bf16 GEMM through torch (hipBLASLt) and a 1 GiB device-to-device copy."""
+    bf16 GEMM through torch (hipBLASLt) and a 1 GiB streaming copy (the
+    library's plain HIP copy kernel, best grid; torch's copy_ beside it)."""
     n = 8192
     gen = torch.Generator(device=dev).manual_seed(0)
     a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=gen)
     b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=gen)
     c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
-    _, kern_ms = _time_gpu(lambda _: torch.matmul(a, b, out=c), steps, warmup)
+    kern_ms = _time_gpu(lambda _: torch.matmul(a, b, out=c), steps, warmup).median_ms
     gemm = 2 * n ** 3 / (kern_ms * 1e-3) / 1e12
     del a, b, c
-    copy = bench_hbm_copy(dev, steps, warmup, 0)["GB_per_s"]
+    stream = bench_hbm_copy(dev, steps, warmup, 0)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch_ms = _time_gpu(lambda _: dst.copy_(src), steps, warmup).median_ms
     return {"gemm_bf16_TFLOP_per_s": gemm, "gemm": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt)",
-            "copy_GB_per_s": copy, "copy": "torch copy_ of 1 GiB (read + write counted)"}
+            "stream_GB_per_s": stream["GB_per_s"],
+            "stream": f"hbm_stream_copy_kernel, 1 GiB, {stream['blocks']} workgroups (read + write counted)",
+            "torch_copy_GB_per_s": 2 * (1 << 30) / (torch_ms * 1e-3) / 1e9}
 
 
 def main():
@@ -567,6 +666,8 @@ def main():
                          "layer, attn_prefill, attn_paged_prefill, attn_decode, hbm_copy")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
+    ap.add_argument("--copy-blocks", type=int, default=None,
+                    help="hbm_copy workload: one grid size (workgroups; 0 = one pass) instead of the sweep")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN path is benchmarked on a single MI355X "
@@ -624,20 +725,21 @@ def main():
         print(f"# attn_decode: {parts['attn_decode']['kernel_ms'] * 1e3:.1f} us/step "
               f"({parts['attn_decode']['GB_per_s']:.0f} GB/s)", file=sys.stderr, flush=True)
     if "hbm_copy" in chosen:
-        parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds)
+        parts["hbm_copy"] = bench_hbm_copy(dev, args.steps, args.warmup, args.cpu_seconds, blocks=args.copy_blocks)
     peaks = None
     if "all" in chosen:
         # each MFMA-bound roofline also as a fraction of a measured library GEMM,
-        # each HBM-bound one as a fraction of the measured copy rate
+        # each HBM-bound one as a fraction of the measured streaming-copy rate
         peaks = measure_peaks(dev, min(args.steps, 20), min(args.warmup, 5))
         for part in parts.values():
             roof = part.get("roofline")
             if roof and roof["bound"] == "mfma":
                 roof["frac_of_measured_gemm"] = roof["achieved"] / peaks["gemm_bf16_TFLOP_per_s"]
             elif roof and roof["bound"] == "hbm":
-                roof["frac_of_measured_copy"] = roof["achieved"] / peaks["copy_GB_per_s"]
+                roof["frac_of_measured_stream"] = roof["achieved"] / peaks["stream_GB_per_s"]
         print(f"# measured peaks: GEMM {peaks['gemm_bf16_TFLOP_per_s']:.0f} TFLOP/s, "
-              f"copy {peaks['copy_GB_per_s']:.0f} GB/s", file=sys.stderr, flush=True)
+              f"stream copy {peaks['stream_GB_per_s']:.0f} GB/s (torch copy_ {peaks['torch_copy_GB_per_s']:.0f})",
+              file=sys.stderr, flush=True)
 
     head_name = "prefill" if "prefill" in parts else next(iter(parts))
     head = parts.pop(head_name)
@@ -660,6 +762,10 @@ def main():
         metric, value, unit = "attention prefill tokens/s", head["tokens_per_s"], "tokens/s"
         workload = (f"flash_attention_varlen: causal, 16 varlen seqs (lengths U[512,4096], seed 0), "
                     f"{head['tokens']} tokens, Hq 16 / Hkv 2, d 256, bf16")
+    elif head_name == "attn_paged_prefill":
+        metric, value, unit = "attention paged prefill tokens/s", head["tokens_per_s"], "tokens/s"
+        workload = ("paged_attention_prefill: 16 seqs, cached prefixes U[0,4096], new chunks U[256,2048], "
+                    "16-token pages, Hq 16 / Hkv 2, d 256, bf16")
     elif head_name == "attn_decode":
         metric, value, unit = "attention paged decode HBM GB/s", head["GB_per_s"], "GB/s"
         workload = ("paged_attention_decode: batch 256, contexts U[512,4096] (602,903 keys), 16-token pages, "

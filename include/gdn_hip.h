@@ -3,7 +3,8 @@
  * Gated DeltaNet linear-attention path.
  *
  * Every entry point takes device pointers wrapped in plain tensor descriptors
- * (pointer, dtype, shape, element strides), launches on the caller's HIP
+ * (pointer, dtype, shape, element strides; gdn_hbm_copy, a measurement
+ * utility, takes plain pointers), launches on the caller's HIP
  * stream, never allocates, never synchronises the host and keeps no global
  * mutable state (one exception: paged_attention_decode_noalloc works in a
  * static device array shared by its calls on a GPU and caches that array's
@@ -282,6 +283,15 @@ int paged_attention_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const
 int paged_attention_decode_noalloc(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
                                    const gdn_tensor* block_tables, const gdn_tensor* context_lens, gdn_tensor* out,
                                    int32_t num_splits, float scale, void* stream);
+
+/*
+ * Measurement utility, no counterpart in the reference: copies nbytes (a
+ * multiple of 16; both pointers 16-byte aligned) from src to dst with a plain
+ * streaming kernel (16-byte non-temporal loads and stores, grid-stride loop
+ * over `blocks` workgroups of 256 threads, 0 = one pass).  The benchmark's
+ * measured HBM ceiling and the calibration of the HBM byte counters.
+ */
+int gdn_hbm_copy(const void* src, void* dst, int64_t nbytes, int32_t blocks, void* stream);
 
 /* Text for any return code of this library. */
 const char* gdn_strerror(int code);

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "paged_attention_decode_workspace_size",
     "paged_attention_decode",
     "paged_attention_decode_noalloc",
+    "gdn_hbm_copy",
     "gdn_strerror",
     "gdn_abi_version",
 )
@@ -113,6 +114,9 @@ def load() -> ctypes.CDLL:
         lib.paged_attention_decode.restype = ctypes.c_int
         lib.paged_attention_decode.argtypes = [_PT] * 7 + [ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]
         lib.paged_attention_decode_noalloc.restype = ctypes.c_int
+        lib.gdn_hbm_copy.restype = ctypes.c_int
+        lib.gdn_hbm_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                     ctypes.c_void_p]
         lib.paged_attention_decode_noalloc.argtypes = [_PT] * 6 + [ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]
         if lib.gdn_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI {lib.gdn_abi_version()}, expected {ABI_VERSION}; rebuild it")

@@ -26,6 +26,7 @@ SOURCES = [
     "causal_conv1d.hip",
     "gdn_norm.hip",
     "attention.hip",
+    "hbm_copy.hip",
     "gdn_capi.cpp",
 ]
 

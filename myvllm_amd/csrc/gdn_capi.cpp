@@ -43,6 +43,7 @@ hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, c
                                     const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
                                     int32_t splits, float scale, hipStream_t st);
 hipError_t attn_decode_scratch(hipStream_t st, float** ptr);
+hipError_t hbm_stream_copy_launch(const void* src, void* dst, int64_t nbytes, int32_t blocks, hipStream_t st);
 
 #define GDN_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -528,4 +529,11 @@ GDN_EXPORT int paged_attention_decode_noalloc(const gdn_tensor* q, const gdn_ten
   }
   return launch_rc(attn_paged_decode_launch(q, k_cache, v_cache, block_tables, context_lens, out, ws, num_splits,
                                             scale, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_hbm_copy(const void* src, void* dst, int64_t nbytes, int32_t blocks, void* stream) {
+  if (nbytes < 0 || nbytes % 16 != 0 || blocks < 0) return GDN_ERR_SHAPE;
+  if (nbytes > 0 && (!src || !dst)) return GDN_ERR_NULL;
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0) return GDN_ERR_ALIGN;
+  return launch_rc(hbm_stream_copy_launch(src, dst, nbytes, blocks, reinterpret_cast<hipStream_t>(stream)));
 }
