@@ -163,6 +163,25 @@ GDN_DEVICE f16x8 frag_cols(const f16_t* M, int ld, int c0, int kbase, int lane) 
   return cat4(__builtin_bit_cast(f16x4, tr_read(p)), __builtin_bit_cast(f16x4, tr_read(p + 8 * ld)));
 }
 
+// K and Q tiles are stored with the middle two 4-element quads of every
+// 16-column group swapped (logical quad q at stored quad kq_quad(q)), so that
+// the 8 k-values a lane takes for one 16-wide k-step (logical columns 4g..4g+3
+// and 8+4g..8+4g+3) are 16 contiguous bytes: one ds_read_b128 per fragment
+// instead of two ds_read_b64 (a wave issues one LDS read per ~35 cycles
+// whatever its width, so the count of reads is what costs).  A Gram of two
+// such tiles needs nothing else; the transposed reads of K (K^T as an A
+// operand, whose rows are K's columns) permute their quad addresses so the
+// lanes still receive logical columns in order.
+GDN_DEVICE int kq_quad(int q) { return ((q & 1) << 1) | (q >> 1); }
+GDN_DEVICE f16x8 frag_rows_kq(const f16_t* M, int r0, int kbase, int lane) {
+  return *reinterpret_cast<const f16x8*>(M + (r0 + (lane & 31)) * LDK + kbase + 8 * (lane >> 5));
+}
+GDN_DEVICE f16x8 frag_cols_kq(const f16_t* M, int c0, int kbase, int lane) {
+  const int j = lane & 15, qd = lane >> 4;
+  const f16_t* p = M + (kbase + 4 * (qd >> 1) + (j >> 2)) * LDK + c0 + 16 * (qd & 1) + 4 * kq_quad(j & 3);
+  return cat4(__builtin_bit_cast(f16x4, tr_read(p)), __builtin_bit_cast(f16x4, tr_read(p + 8 * LDK)));
+}
+
 // Per-row vector entries for C-layout rows r0 + 8i + 4g + (0..3).
 GDN_DEVICE f32x4 rows4(const float* vec, int r0, int i, int lane) {
   return *reinterpret_cast<const f32x4*>(vec + r0 + 8 * i + 4 * (lane >> 5));
@@ -565,7 +584,7 @@ GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, in
   f32x16 G = zero16();
 #pragma unroll
   for (int ks = 0; ks < KD / 16; ++ks)
-    G = mfma32(frag_rows(M1, LDK, 32 * mt, 16 * ks, lane), frag_rows(M2, LDK, 32 * nt, 16 * ks, lane), G);
+    G = mfma32(frag_rows_kq(M1, 32 * mt, 16 * ks, lane), frag_rows_kq(M2, 32 * nt, 16 * ks, lane), G);
   return G;
 }
 
@@ -757,9 +776,17 @@ GDN_DEVICE void p_tile(ChunkTiles& ct, int mt, int nt, int lane) {
 
 // Stage a tile held in registers into LDS (fp16 for K/Q, bf16 as is for V).
 GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane) {
+  // lane's 8 logical columns 8a..8a+7 (a = lane % 16) are quads 2a', 2a'+1 of
+  // 16-column group a / 2 (a' = a % 2), stored at quads kq_quad(2a'), kq_quad(2a'+1)
+  const int a = lane & 15, grp = 16 * (a >> 1), q0 = 2 * (a & 1);
+  const int off0 = grp + 4 * kq_quad(q0), off1 = grp + 4 * kq_quad(q0 + 1);
 #pragma unroll
-  for (int u = 0; u < 16; ++u)
-    *reinterpret_cast<f16x8*>(dst + ((lane >> 4) + 4 * u) * LDK + 8 * (lane & 15)) = bf16x8_to_f16x8(tl.r[u]);
+  for (int u = 0; u < 16; ++u) {
+    const f16x8 v = bf16x8_to_f16x8(tl.r[u]);
+    f16_t* row = dst + ((lane >> 4) + 4 * u) * LDK;
+    *reinterpret_cast<f16x4*>(row + off0) = (f16x4){v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f16x4*>(row + off1) = (f16x4){v[4], v[5], v[6], v[7]};
+  }
 }
 GDN_DEVICE void stage_v(bf16_t* dst, const TileLoad& tl, int lane) {
 #pragma unroll
@@ -814,10 +841,10 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
   for (int ks = 0; ks < 8; ++ks) {
     f16x8 shi, slo;
     split8u(S[ks >> 1], ks & 1, one, shi, slo);
-    const f16x8 ak0 = frag_rows(ct.k, LDK, 0, 16 * ks, lane);
-    const f16x8 ak1 = frag_rows(ct.k, LDK, 32, 16 * ks, lane);
-    const f16x8 aq0 = frag_rows(ct.q, LDK, 0, 16 * ks, lane);
-    const f16x8 aq1 = frag_rows(ct.q, LDK, 32, 16 * ks, lane);
+    const f16x8 ak0 = frag_rows_kq(ct.k, 0, 16 * ks, lane);
+    const f16x8 ak1 = frag_rows_kq(ct.k, 32, 16 * ks, lane);
+    const f16x8 aq0 = frag_rows_kq(ct.q, 0, 16 * ks, lane);
+    const f16x8 aq1 = frag_rows_kq(ct.q, 32, 16 * ks, lane);
     X[0] = mfma32(ak0, shi, X[0]);
     X[1] = mfma32(ak1, shi, X[1]);
     QS[0] = mfma32(aq0, shi, QS[0]);
@@ -968,7 +995,7 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
     split8f(VN[ks >> 1], ks & 1, fd, dhi, dlo);
     f16x8 akt[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols(ct.k, LDK, 32 * mt, 16 * ks, lane);
+    for (int mt = 0; mt < 4; ++mt) akt[mt] = frag_cols_kq(ct.k, 32 * mt, 16 * ks, lane);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) U[mt] = mfma32(akt[mt], dhi, ks == 0 ? zero16() : U[mt]);
 #pragma unroll
