@@ -105,20 +105,21 @@ int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tenso
 /*
  * Chunked gated-delta-rule prefill over packed varlen sequences (replaces
  * chunk_gated_delta_rule, ops/gated_delta_rule/gated_delta_rule.py:31-66).
- *   q, k   : (T, Hk, K)  bf16, last stride 1, token/head strides multiples of 8
- *   v      : (T, Hv, V)  bf16, same constraints
+ *   q, k   : (T, Hk, K)  bf16|f16, last stride 1, token/head strides multiples of 8
+ *   v      : (T, Hv, V)  same dtype as q, same constraints
  *   g      : (T, Hv)     f32   natural-log decay per token and v-head
  *   beta   : (T, Hv)     f32|bf16|f16
  *   state  : (S, Hv, K, V) f32; initial state read from state[idx[n]], final
  *            state written back there
  *   state_indices : (N,) i32|i64
  *   cu_seqlens    : (N+1,) i32|i64
- *   out    : (T, Hv, V)  bf16, last stride 1
+ *   out    : (T, Hv, V)  v's dtype, last stride 1
  * chunk_size must be 64; K = V = 128.  Tokens not covered by any sequence
  * keep whatever `out` held.
  * Range: the MFMA operands are fp16, so every q and k row must have an L2
  * norm of at most 128 (the layer's rows are L2-normalised, norm 1) and |v|
- * entries must stay below 65504; the state may have any magnitude (it is
+ * entries must stay below 65504 (an fp16 out also overflows past 65504, as
+ * the reference's fp16 output would); the state may have any magnitude (it is
  * held in per-column power-of-two units).  Keys of any norm in that range
  * keep the fp32 state bound (the state-update split is sized from each
  * chunk's largest key norm).

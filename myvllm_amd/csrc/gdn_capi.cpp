@@ -131,7 +131,8 @@ int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* 
   if (k->dtype != q->dtype || v->dtype != q->dtype || out->dtype != v->dtype) return GDN_ERR_DTYPE;
   if (!is_float(q->dtype) || !is_float(g->dtype) || !is_float(beta->dtype)) return GDN_ERR_DTYPE;
   if (state->dtype != GDN_DTYPE_F32 || !is_index(idx->dtype)) return GDN_ERR_DTYPE;
-  if (prefill && (q->dtype != GDN_DTYPE_BF16 || g->dtype != GDN_DTYPE_F32 || !is_index(cu->dtype)))
+  if (prefill && ((q->dtype != GDN_DTYPE_BF16 && q->dtype != GDN_DTYPE_F16) || g->dtype != GDN_DTYPE_F32 ||
+                  !is_index(cu->dtype)))
     return GDN_ERR_DTYPE;
 
   // head dims

@@ -563,6 +563,39 @@ GDN_DEVICE f16x8 bf16x8_to_f16x8(bf16x8 x) {
   return __builtin_bit_cast(f16x8, o);
 }
 
+// The kernel reads q/k/v and writes o as 16-bit floats of one type: bf16
+// (F16 = false) or fp16 (F16 = true).  Loads and the V tile move raw bits;
+// these convert at the points of use.
+template <bool F16>
+GDN_DEVICE f16x8 to_f16x8(bf16x8 raw) {
+  if constexpr (F16) return __builtin_bit_cast(f16x8, raw);
+  else return bf16x8_to_f16x8(raw);
+}
+template <bool F16>
+GDN_DEVICE f32x4 to_f32x4(s16x4 raw) {
+  f32x4 r;
+  if constexpr (F16) {
+    const f16x4 h = __builtin_bit_cast(f16x4, raw);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) r[m] = (float)h[m];
+  } else {
+    const bf16x4 h = __builtin_bit_cast(bf16x4, raw);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) r[m] = (float)h[m];
+  }
+  return r;
+}
+template <bool F16>
+GDN_DEVICE s16x4 from_f32x4(f32x4 x) {
+  if constexpr (F16) {
+    const f16x4 h = {(f16_t)x[0], (f16_t)x[1], (f16_t)x[2], (f16_t)x[3]};
+    return __builtin_bit_cast(s16x4, h);
+  } else {
+    const bf16x4 h = {(bf16_t)x[0], (bf16_t)x[1], (bf16_t)x[2], (bf16_t)x[3]};
+    return __builtin_bit_cast(s16x4, h);
+  }
+}
+
 // gamma = in-chunk cumsum of g (one token per lane) and the per-token decay
 // vectors; g and beta of tokens past the chunk end are taken as zero.
 // Whether every lane's |gamma| < 80, so that e^gamma and e^-gamma are both
@@ -588,11 +621,20 @@ GDN_DEVICE f32x16 gram_tile(const f16_t* M1, const f16_t* M2, int mt, int nt, in
   return G;
 }
 
-// kk^T of a diagonal block's rows from the register fragments (bf16 holds k exactly)
+// kk^T of a diagonal block's rows from the register fragments, in k's own
+// 16-bit type (which holds k exactly)
+template <bool F16>
 GDN_DEVICE f32x16 gram_regs(const bf16x8 (&kf)[8]) {
   f32x16 G = zero16();
 #pragma unroll
-  for (int ks = 0; ks < KD / 16; ++ks) G = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], kf[ks], G, 0, 0, 0);
+  for (int ks = 0; ks < KD / 16; ++ks) {
+    if constexpr (F16) {
+      const f16x8 h = __builtin_bit_cast(f16x8, kf[ks]);
+      G = mfma32(h, h, G);
+    } else {
+      G = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], kf[ks], G, 0, 0, 0);
+    }
+  }
   return G;
 }
 
@@ -774,7 +816,9 @@ GDN_DEVICE void p_tile(ChunkTiles& ct, int mt, int nt, int lane) {
   }
 }
 
-// Stage a tile held in registers into LDS (fp16 for K/Q, bf16 as is for V).
+// Stage a tile held in registers into LDS (fp16 for K/Q, the raw 16-bit
+// elements for V).
+template <bool F16>
 GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane) {
   // lane's 8 logical columns 8a..8a+7 (a = lane % 16) are quads 2a', 2a'+1 of
   // 16-column group a / 2 (a' = a % 2), stored at quads kq_quad(2a'), kq_quad(2a'+1)
@@ -782,7 +826,7 @@ GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane) {
   const int off0 = grp + 4 * kq_quad(q0), off1 = grp + 4 * kq_quad(q0 + 1);
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
-    const f16x8 v = bf16x8_to_f16x8(tl.r[u]);
+    const f16x8 v = to_f16x8<F16>(tl.r[u]);
     f16_t* row = dst + ((lane >> 4) + 4 * u) * LDK;
     *reinterpret_cast<f16x4*>(row + off0) = (f16x4){v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f16x4*>(row + off1) = (f16x4){v[4], v[5], v[6], v[7]};
@@ -825,6 +869,7 @@ GDN_DEVICE int out_slot(int s, int m) {
 // mixes value columns): the update rescales S by one factor per chunk and
 // picks the new units from the exponents of V' and of the decayed state, so
 // S stays below 2^14 and is split without another pass over it.
+template <bool F16>
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, bf16_t* vt, int32_t* v_free,
                               f32x16 (&S)[4], int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h,
                               int wave, int lane) {
@@ -867,10 +912,10 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
       const f32x4 bv = rows4(ct.beta, 32 * mt, i, lane);
       const int j = lane & 15, qd = lane >> 4;
       const bf16_t* p = vt + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
-      const bf16x4 vv = __builtin_bit_cast(bf16x4, tr_read(p));
+      const f32x4 vv = to_f32x4<F16>(tr_read(p));
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu * bv[rr]), X[mt][4 * i + rr], (float)vv[rr] * bv[rr]);
+        X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu * bv[rr]), X[mt][4 * i + rr], vv[rr] * bv[rr]);
     }
   }
   f32x16* R = X;  // X now holds R
@@ -932,10 +977,10 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        bf16x4 o4;
+        f32x4 o4;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o4[rr] = (bf16_t)(QS[mt][4 * i + rr] * osc);
-        *reinterpret_cast<bf16x4*>(vt + (2 * n + mt) * LDV + 32 * wave + 4 * out_slot(2 * i + gq, n)) = o4;
+        for (int rr = 0; rr < 4; ++rr) o4[rr] = QS[mt][4 * i + rr] * osc;
+        *reinterpret_cast<s16x4*>(vt + (2 * n + mt) * LDV + 32 * wave + 4 * out_slot(2 * i + gq, n)) = from_f32x4<F16>(o4);
       }
     // lane (qd, j) of the four 16-lane groups: output row 16 u + j, columns 8 qd .. 8 qd + 7
     const int j = lane & 15, qd = lane >> 4;
@@ -1025,6 +1070,7 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
   su = ed;
 }
 
+template <bool F16>
 __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
   __shared__ Smem sm;
 
@@ -1087,7 +1133,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     }
     __syncthreads();  // chunk 0 is prepared
     for (int c = 0; c < nc; ++c) {
-      consume_chunk(sm.tiles[c & 1], sm.tb[c % 3], fmaxf(sm.kn2[c % 3][0], sm.kn2[c % 3][1]), sm.v, &sm.v_free, S,
+      consume_chunk<F16>(sm.tiles[c & 1], sm.tb[c % 3], fmaxf(sm.kn2[c % 3][0], sm.kn2[c % 3][1]), sm.v, &sm.v_free, S,
                     su, sb, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
       // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
       if ((c & 15) == 15) sb = col_max(S, 4);
@@ -1097,11 +1143,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       // a producer wait gave up: NaN in every output row of this item (this
       // wave's 32 columns), state slot untouched
       asm volatile("");
-      const bf16_t nan = (bf16_t)__builtin_nanf("");
+      const s16x4 nan4 = from_f32x4<F16>((f32x4){__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")});
+      const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3], nan4[0], nan4[1], nan4[2], nan4[3]});
       for (int64_t t = s + (lane >> 2); t < e; t += 16) {
-        bf16x8 z;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) z[m] = nan;
         *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
       }
       return;
@@ -1143,7 +1187,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       dieg[lane] = __expf(-gm);
       const bool fact = factorable(gm);
       dbeta[lane] = lane < L ? scalar_raw_f32(dl.d.b, a.b_dtype) : 0.f;
-      const f32x16 G = gram_regs(dl.kf);
+      const f32x16 G = gram_regs<F16>(dl.kf);
       // max_i |k_i|^2 over this block's rows: the largest |k_i.k_j| of the Gram (Cauchy-Schwarz)
       {
         float m = 0.f;
@@ -1176,7 +1220,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     // K tile and decay vectors of chunk c into tile set c & 1, then release wave 7
     auto stage = [&](int c) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[c & 1];
-      stage_f16(ct.k, kl, lane);
+      stage_f16<F16>(ct.k, kl, lane);
       stage_decay(ct, dl, chunk_len(c), a.b_dtype, lane);
       producer_arrive(&sm.kv_ready, lane);
     };
@@ -1206,7 +1250,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     // Q tile and the three P tiles of chunk c
     auto qp = [&](int c) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[c & 1];
-      stage_f16(ct.q, ql, lane);
+      stage_f16<F16>(ct.q, ql, lane);
       if (c + 1 < nc) qload(c + 1);
       producer_wait(&sm.kv_ready, c + 1, a.spin_limit, &sm.failed);
       p_tile(ct, 0, 0, lane);
@@ -1269,6 +1313,9 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   const int64_t nwork = a.nseq * a.Hv;
   if (nwork == 0 || a.T == 0) return hipSuccess;
   const int64_t nblocks = (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
-  gdn_chunk_prefill_kernel<<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
+  if (q->dtype == GDN_DTYPE_F16)
+    gdn_chunk_prefill_kernel<true><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
+  else
+    gdn_chunk_prefill_kernel<false><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
   return hipGetLastError();
 }

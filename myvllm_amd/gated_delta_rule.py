@@ -28,9 +28,9 @@ def _lastdim_contiguous(t: torch.Tensor) -> torch.Tensor:
 
 
 def chunk_gated_delta_rule(
-    q: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) bf16
-    k: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) bf16
-    v: torch.Tensor,  # (total_tokens, num_v_heads, v_head_dim) bf16
+    q: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) bf16 or fp16
+    k: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) q's dtype
+    v: torch.Tensor,  # (total_tokens, num_v_heads, v_head_dim) q's dtype
     g: torch.Tensor,  # (total_tokens, num_v_heads) fp32 log-decay
     beta: torch.Tensor,  # (total_tokens, num_v_heads)
     recurrent_state: torch.Tensor,  # (max_seq_cnt, num_v_heads, k_head_dim, v_head_dim) fp32

@@ -113,7 +113,7 @@ def test_prefill_validation():
     assert _call_prefill(a, torch.tensor([0, 10], dtype=torch.int32)) == ERR["SHAPE"]  # idx has 2 entries
     b = _recurrent_args(B=10, dtype=torch.float32)
     b["idx"] = torch.zeros(2, dtype=torch.int32)
-    assert _call_prefill(b, cu) == ERR["DTYPE"]  # prefill takes bf16 q/k/v only
+    assert _call_prefill(b, cu) == ERR["DTYPE"]  # prefill takes bf16 or fp16 q/k/v only
     c = _recurrent_args(B=10, K=64, V=64)
     c["idx"] = torch.zeros(2, dtype=torch.int32)
     assert _call_prefill(c, cu) == ERR["HEAD_DIM"]

@@ -207,6 +207,33 @@ def test_prefill_more_than_256_sequences(dev):
     _check(case, o, st, o_ref, st_ref)
 
 
+@pytest.mark.parametrize("lengths,g_scale", [([5, 64, 65, 200], 1.0), ([300, 1000], 0.01)])
+def test_prefill_fp16(dev, lengths, g_scale):
+    """fp16 q/k/v (the reference's prefill follows the inputs' dtype,
+    ops/gated_delta_rule/wu.py:150-151, o.py:147): o comes back in fp16, the
+    state within the same bound; the oracle runs in fp64 on the fp16 inputs."""
+    case = prefill_case(lengths, seed=31, num_slots=6, Hk=2, Hv=4, g_scale=g_scale, dtype=torch.float16)
+    o, st, o_ref, st_ref = _run(case, dev)
+    assert o.dtype == torch.float16
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_fp16_matches_bf16_rounded_inputs(dev):
+    """The same values through both kernels: bf16 inputs converted exactly to
+    fp16 give the bf16 run's state to fp32 rounding and its output to bf16
+    rounding."""
+    case = prefill_case([130, 64], seed=32, num_slots=3, Hk=2, Hv=4)
+    st_b, st_h = case.state.to(dev), case.state.to(dev)
+    args = [t.to(dev) for t in (case.g, case.beta)]
+    idx, cu = case.idx.to(dev), case.cu.to(dev)
+    o_b = chunk_gated_delta_rule(case.q.to(dev), case.k.to(dev), case.v.to(dev), *args, st_b, idx, cu)
+    o_h = chunk_gated_delta_rule(case.q.to(dev).half(), case.k.to(dev).half(), case.v.to(dev).half(), *args, st_h, idx, cu)
+    torch.cuda.synchronize()
+    assert o_h.dtype == torch.float16
+    torch.testing.assert_close(o_h.float().cpu(), o_b.float().cpu(), rtol=1e-2, atol=1e-3)
+    torch.testing.assert_close(st_h.cpu(), st_b.cpu(), rtol=1e-5, atol=1e-6)
+
+
 def test_prefill_wait_give_up_poisons_the_item(dev, monkeypatch):
     """The kernel's waits between its wave roles are bounded; one that gives
     up must not pass as a plausible answer.  Forced from the host (spin limit
