@@ -54,7 +54,8 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # from the committed profiles of the current kernels (profiles/*.md, which
 # give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_026_275_700,
+    "gdn_chunk_prefill_kernel": 1_025_893_376,
+    "gdn_chunk_prefill_kernel/short": 3_020_943_155,
     "gdn_recurrent_step_kernel": 1_083_199_150,
     "causal_conv1d_varlen_kernel": 665_974_958,
     "causal_conv1d_step_kernel": 59_313_861,
@@ -244,6 +245,57 @@ def bench_prefill(dev, steps, warmup, cpu_budget):
                                                            case.cu, dtype=torch.float32), cpu_budget)
         res["cpu_baseline"] = _cpu_baseline(T / sec, "tokens/s",
                                             f"full workload ({T} tokens), fp32 chunked (C=64) torch restatement")
+    return res
+
+
+def prefill_bytes(case) -> int:
+    """Algorithmic HBM bytes of one prefill launch: q, k, v and g, beta read,
+    o written, and each (sequence, v-head) state read and written once."""
+    el = lambda t: t.numel() * t.element_size()
+    n_state = case.idx.numel() * case.state.shape[1] * case.state.shape[2] * case.state.shape[3] * 4
+    return el(case.q) + el(case.k) + 2 * el(case.v) + el(case.g) + el(case.beta) + 2 * n_state
+
+
+def bench_prefill_short(dev, steps, warmup, cpu_budget):
+    from myvllm_amd import chunk_gated_delta_rule
+    from myvllm_amd.workloads import prefill_short_case
+
+    case = prefill_short_case()
+    T = case.tokens
+    q, k, v, g, beta, state, idx, cu = (t.to(dev) for t in (case.q, case.k, case.v, case.g, case.beta,
+                                                             case.state, case.idx, case.cu))
+
+    def step(_):
+        chunk_gated_delta_rule(q, k, v, g, beta, state, idx, cu)
+
+    tm = _time_gpu(step, steps, warmup)
+    ms, kern_ms = tm.step_ms, tm.median_ms
+    nbytes = prefill_bytes(case)
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "tokens": T, "sequences": int(case.idx.numel()),
+        "ms_per_step": ms,
+        "kernel_ms": kern_ms, "kernel_ms_mean": tm.mean_ms,
+        "tokens_per_s": T / (ms * 1e-3),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": _traffic("gdn_chunk_prefill_kernel/short"),
+                     "bytes_per_launch": nbytes, "kernel": "gdn_chunk_prefill_kernel",
+                     "mfma_TFLOP_per_s": PREFILL_FLOP_PER_TOKEN * T / (kern_ms * 1e-3) / 1e12},
+    }
+    if cpu_budget > 0:
+        from oracle.gdn import chunk_gated_delta_rule_ref
+
+        _cpu_setup()
+        n = 64  # a bounded sample: the first 64 sequences
+        cu_s = case.cu[: n + 1]
+        Ts = int(cu_s[-1])
+        st = case.state.clone()
+        sec = _time_cpu(lambda: chunk_gated_delta_rule_ref(case.q[:Ts], case.k[:Ts], case.v[:Ts], case.g[:Ts],
+                                                           case.beta[:Ts], st, case.idx[:n], cu_s,
+                                                           dtype=torch.float32), cpu_budget)
+        res["cpu_baseline"] = _cpu_baseline(Ts / sec, "tokens/s",
+                                            f"first {n} of the {case.idx.numel()} sequences ({Ts} tokens), "
+                                            "fp32 chunked (C=64) torch restatement")
     return res
 
 
@@ -662,7 +714,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="all",
-                    help="all, or a comma-separated list of prefill, decode, conv, conv_update, decode_fused, "
+                    help="all, or a comma-separated list of prefill, prefill_short, decode, conv, conv_update, "
+                         "decode_fused, "
                          "layer, attn_prefill, attn_paged_prefill, attn_decode, hbm_copy")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
@@ -681,7 +734,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    known = {"prefill", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill",
+    known = {"prefill", "prefill_short", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill",
              "attn_paged_prefill", "attn_decode", "hbm_copy"}
     chosen = set(args.workload.split(","))
     if not chosen <= (known | {"all"}):
@@ -692,6 +745,10 @@ def main():
     if want("prefill"):
         parts["prefill"] = bench_prefill(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# prefill: {parts['prefill']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    if want("prefill_short"):
+        parts["prefill_short"] = bench_prefill_short(dev, args.steps, args.warmup, args.cpu_seconds)
+        print(f"# prefill_short: {parts['prefill_short']['kernel_ms'] * 1e3:.1f} us/launch "
+              f"({parts['prefill_short']['roofline']['achieved']:.0f} GB/s)", file=sys.stderr, flush=True)
     if want("decode"):
         parts["decode"] = bench_decode(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# decode: {parts['decode']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
@@ -747,6 +804,10 @@ def main():
         metric, value, unit = "GDN prefill tokens/s", head["tokens_per_s"], "tokens/s"
         workload = (f"gdn_chunk_prefill: 16 varlen seqs (lengths U[512,4096], seed 0), {head['tokens']} tokens, "
                     f"Hk {HK} / Hv {HV}, d {DK}, chunk {CHUNK}, bf16 q/k/v, fp32 g/beta/state")
+    elif head_name == "prefill_short":
+        metric, value, unit = "GDN prefill tokens/s", head["tokens_per_s"], "tokens/s"
+        workload = (f"gdn_chunk_prefill: {head['sequences']} sequences of 64 tokens ({head['tokens']} tokens), "
+                    f"Hk {HK} / Hv {HV}, d {DK}, bf16 q/k/v, fp32 g/beta/state")
     elif head_name == "decode":
         metric, value, unit = "GDN decode state-update HBM GB/s", head["GB_per_s"], "GB/s"
         workload = "gdn_recurrent_step: batch 256 from a 1024-slot fp32 state cache, Hk 16 / Hv 32, d 128"

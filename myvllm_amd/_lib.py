@@ -1,8 +1,10 @@
 """ctypes binding of libgdn_hip.so (the C ABI declared in include/gdn_hip.h).
 
 The library is loaded from the package's ``lib/`` directory; it is built
-in-tree by ``myvllm_amd.build.build()``.  There is no fallback: if the library
-is missing every op raises.
+in-tree by ``myvllm_amd.build.build()``.  ``MYVLLM_AMD_LIB`` in the environment
+names another build of the same library instead (the host-AddressSanitizer
+build of ``myvllm_amd.build.build_asan()``, for the C-ABI tests).  There is no
+fallback: if the library is missing every op raises.
 """
 from __future__ import annotations
 
@@ -12,7 +14,8 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libgdn_hip.so")
+LIB_PATH = os.environ.get("MYVLLM_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
+                                                            "libgdn_hip.so")
 ABI_VERSION = 1
 MAX_NDIM = 4
 

@@ -95,5 +95,45 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     return out
 
 
+ASAN_LIBNAME = "libgdn_hip_asan.so"
+# Host-only AddressSanitizer for the C-ABI layer: every -fsanitize flag goes
+# after -Xarch_host, so the device code of the kernels is built as usual.
+ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
+                   "-Xarch_host", "-shared-libsan"]
+
+
+def asan_runtime() -> str:
+    """The compiler's shared AddressSanitizer runtime (to preload into a host
+    process that loads the instrumented library)."""
+    res = subprocess.run([_hipcc(), "--print-file-name=libclang_rt.asan-x86_64.so"], stdout=subprocess.PIPE,
+                         stderr=subprocess.DEVNULL, text=True)
+    path = res.stdout.strip()
+    if not os.path.isabs(path) or not os.path.exists(path):
+        raise RuntimeError("the AddressSanitizer runtime libclang_rt.asan-x86_64.so was not found")
+    return path
+
+
+def build_asan(verbose: bool = False) -> str:
+    """libgdn_hip_asan.so: gdn_capi.cpp (argument validation, the C ABI)
+    compiled with host AddressSanitizer, linked with the kernels' objects of
+    the last build(); returns its path.  Load it through MYVLLM_AMD_LIB with
+    asan_runtime() preloaded."""
+    hipcc = _hipcc()
+    objs = []
+    for src in SOURCES:
+        obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+        if src == "gdn_capi.cpp":
+            obj = os.path.join(OBJDIR, "gdn_capi_asan.o")
+            _run([hipcc, *COMMON_FLAGS, *ASAN_HOST_FLAGS, "-g", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        elif not os.path.exists(obj):
+            raise RuntimeError(f"{obj} is missing: run build() first")
+        objs.append(obj)
+    out = os.path.join(LIBDIR, ASAN_LIBNAME)
+    tmp = out + f".tmp{os.getpid()}"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *ASAN_HOST_FLAGS, "-o", tmp, *objs], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build_asan(verbose="-v" in sys.argv) if "--asan" in sys.argv else build(verbose="-v" in sys.argv))

@@ -92,6 +92,15 @@ def prefill_32k_case(seed: int = 0) -> PrefillCase:
     return prefill_case(lengths, seed=seed + 1, num_slots=64)
 
 
+def prefill_short_case(seed: int = 0) -> PrefillCase:
+    """Many short sequences, as a chunked-prefill scheduler sends them: 512
+    sequences of 64 tokens (32,768 tokens, one chunk each), Hk 16 / Hv 32,
+    d 128, bf16 q/k/v, fp32 g/beta, fp32 initial state ~N(0, 0.1) in a
+    512-slot cache.  Each (sequence, v-head) reads and writes its 64 KiB state
+    once per 64 tokens, so the state traffic dominates."""
+    return prefill_case([64] * 512, seed=seed + 5, num_slots=512)
+
+
 @dataclass
 class DecodeCase:
     q: torch.Tensor
