@@ -30,9 +30,11 @@
 //   O  = scale [diag(e^gamma) Q S + P V']
 //   S  = e^gamma_L S + K^T diag(e^(gamma_L - gamma)) V'
 //
-// The MFMAs run in fp16 (same rate as bf16): q and k are L2-normalised bf16
-// values, which fp16 holds exactly, and every fp32 operand that feeds the
-// carried state (S, R, the decayed V', T, A_10 and the merge product) is
+// The MFMAs run in fp16 (same rate as bf16).  q and k are bf16 or fp16
+// values; fp16 holds a bf16 value exactly when |x| >= 2^-14 (its normal
+// range) and rounds smaller components to its subnormal grid (absolute error
+// <= 2^-25, nothing next to a row of norm ~1).  Every fp32 operand that feeds
+// the carried state (S, R, the decayed V', T, A_10 and the merge product) is
 // split into fp16 hi + lo parts (22 mantissa bits; lo x lo is dropped).  R
 // and V' are first scaled by a power of two per value column (max |x| in
 // [2^9, 2^10)) so fp16 can neither overflow nor flush them; the scale is
