@@ -18,7 +18,7 @@ hipError_t gdn_recurrent_step_launch(const gdn_tensor* q, const gdn_tensor* k, c
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    int32_t spin_limit, hipStream_t st);
+                                    int32_t spin_limit, int32_t items_per_wg, hipStream_t st);
 hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
                                        int64_t norm_ch, hipStream_t st);
@@ -266,6 +266,19 @@ int32_t prefill_spin_limit() {
   return (end && *end == 0 && v >= 0 && v <= kDefault) ? (int32_t)v : kDefault;
 }
 
+// Items (sequence, v-head) per prefill workgroup: -1 lets the launcher choose
+// (several consecutive items per workgroup for batches of short sequences,
+// one otherwise).  GDN_PREFILL_ITEMS_PER_WG in the environment fixes it (0: one
+// item per workgroup, longest first; 1..64: that many consecutive items), so
+// that a test can run both schedules on the same inputs.
+int32_t prefill_items_per_wg() {
+  const char* env = std::getenv("GDN_PREFILL_ITEMS_PER_WG");
+  if (!env || !*env) return -1;
+  char* end = nullptr;
+  const long v = std::strtol(env, &end, 10);
+  return (end && *end == 0 && v >= 0 && v <= 64) ? (int32_t)v : -1;
+}
+
 constexpr int64_t kMaxGridYZ = 65535;
 constexpr int32_t kMaxDecodeSplits = 256;
 
@@ -345,7 +358,8 @@ GDN_EXPORT int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const
   if (chunk_size != 64) return GDN_ERR_CHUNK;
   GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, cu_seqlens, true));
   return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale,
-                                            prefill_spin_limit(), reinterpret_cast<hipStream_t>(stream)));
+                                            prefill_spin_limit(), prefill_items_per_wg(),
+                                            reinterpret_cast<hipStream_t>(stream)));
 }
 
 GDN_EXPORT int causal_conv1d_varlen(const gdn_tensor* x, const gdn_tensor* weight, gdn_tensor* conv_state,

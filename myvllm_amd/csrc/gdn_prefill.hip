@@ -81,6 +81,7 @@ struct PrefillArgs {
   int32_t b_dtype;
   float scale;
   int32_t spin_limit;  // bound of a producer wait (sleep iterations)
+  int32_t per_wg;      // items per workgroup: 0 = one item, longest first; else consecutive work ids
   bool idx64, cu64;
 };
 
@@ -1072,19 +1073,91 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
   su = ed;
 }
 
-template <bool F16>
+// ---- the workgroup's items and its chunk stream -------------------------------
+//
+// A workgroup processes one item (sequence, v-head) or, for batches of many
+// short sequences, up to 64 consecutive items: item j's fields sit in lane j
+// of every wave and are read with readlane.  All roles walk the same stream of
+// (item, chunk) positions, so the producers stage and solve the next item's
+// first chunks while the state waves still work on the current item.
+struct Items {
+  int64_t s, e;  // token range of the lane's item
+  int32_t slot;  // its state slot, -1 for a padding sequence
+  int32_t h;     // its v-head
+  int32_t nc;    // its chunks (0: empty or padding, no state work)
+  int m;         // items of the workgroup (uniform)
+};
+GDN_DEVICE int32_t rd32(int32_t x, int j) { return __builtin_amdgcn_readlane(x, j); }
+GDN_DEVICE int64_t rd64(int64_t x, int j) {
+  const uint64_t u = (uint64_t)x;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int32_t)(uint32_t)u, j);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int32_t)(uint32_t)(u >> 32), j);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// Position in the stream: chunk c of item j (j == m: past the end).
+struct Pos {
+  int j, c;
+};
+GDN_DEVICE Pos skip_empty(const Items& it, Pos p) {
+  while (p.j < it.m && rd32(it.nc, p.j) == 0) ++p.j;
+  return p;
+}
+GDN_DEVICE Pos next_pos(const Items& it, Pos p) {
+  if (++p.c >= rd32(it.nc, p.j)) {
+    p.c = 0;
+    ++p.j;
+    p = skip_empty(it, p);
+  }
+  return p;
+}
+struct ChunkAt {
+  int64_t c0, e;  // first token of the chunk, end of its sequence
+  int L, h;       // tokens in the chunk, v-head
+  int32_t slot;
+};
+GDN_DEVICE ChunkAt chunk_at(const Items& it, Pos p) {
+  ChunkAt ch;
+  ch.e = rd64(it.e, p.j);
+  ch.c0 = rd64(it.s, p.j) + (int64_t)p.c * C;
+  const int64_t r = ch.e - ch.c0;
+  ch.L = (int)(r < C ? r : C);
+  ch.h = rd32(it.h, p.j);
+  ch.slot = rd32(it.slot, p.j);
+  return ch;
+}
+GDN_DEVICE ChunkSource source_of(const PrefillArgs& a, const ChunkAt& ch) {
+  const int kh = ch.h / a.r;
+  return {&a, a.k + kh * a.k_s1, a.q + kh * a.q_s1, a.v + ch.h * a.v_s1, ch.h, ch.e};
+}
+// Item fields of (sequence, v-head) = (seq, h).
+GDN_DEVICE void item_fields(const PrefillArgs& a, int64_t seq, int h, Items& it) {
+  seq_range(a.cu, a.cu64, seq, a.T, it.s, it.e);
+  const int64_t slot = load_index(a.idx, seq, a.idx64);
+  const bool pad = slot < 0 || slot >= a.num_slots;
+  it.slot = pad ? -1 : (int32_t)slot;
+  it.h = h;
+  it.nc = (pad || it.e <= it.s) ? 0 : (int32_t)((it.e - it.s + C - 1) / C);
+}
+
+// MULTI: several items per workgroup (a.per_wg > 0); the one-item schedule
+// is its own instantiation, so the long-sequence path pays nothing for the
+// item stream.
+template <bool F16, bool MULTI>
 __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
   __shared__ Smem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-
-  // Work id: consecutive v-heads (sharing a k-head) go to one XCD (workgroups
-  // are dealt round-robin over the 8 XCDs), sequences longest first.
   const int64_t bid = blockIdx.x;
-  const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
-  if (work >= a.nseq * a.Hv) return;
+  const int64_t nwork = a.nseq * a.Hv;
+
+  // One item per workgroup: consecutive v-heads (sharing a k-head) go to one
+  // XCD (workgroups are dealt round-robin over the 8 XCDs), sequences longest
+  // first.  Several items per workgroup: a contiguous run of work ids, whose
+  // v-head pairs then share the workgroup's L2.
+  const int64_t work = MULTI ? bid * a.per_wg : 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
+  if (work >= nwork) return;
   if (tid == 0) {
     sm.kv_ready = 0;
     sm.v_free = 0;
@@ -1092,97 +1165,131 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     sm.failed = 0;
   }
   __syncthreads();  // the counters are zero before any wave can arrive
-  const int64_t seq = seq_of_rank(sm, a, work / a.Hv, tid);
-  const int h = (int)(work % a.Hv);
-  const int kh = h / a.r;
-  int64_t s, e;
-  seq_range(a.cu, a.cu64, seq, a.T, s, e);
-  if (e <= s) return;
-  const int64_t slot = load_index(a.idx, seq, a.idx64);
-  if (slot < 0 || slot >= a.num_slots) {  // padding sequence: zero output rows, no state
+  Items it;
+  if (!MULTI) {
+    it.m = 1;
+    item_fields(a, seq_of_rank(sm, a, work / a.Hv, tid), (int)(work % a.Hv), it);
+  } else {
+    const int64_t left = nwork - work;
+    it.m = (int)(left < a.per_wg ? left : a.per_wg);
+    const int64_t w = work + (lane < it.m ? lane : 0);
+    item_fields(a, w / a.Hv, (int)(w % a.Hv), it);
+  }
+  // padding sequences: zero output rows, no state
+  for (int j = 0; j < it.m; ++j) {
+    if (rd32(it.slot, j) >= 0) continue;
+    const int64_t s = rd64(it.s, j), e = rd64(it.e, j);
+    const int h = rd32(it.h, j);
     for (int64_t t = s + (tid >> 4); t < e; t += kThreads / 16) {
       bf16x8 z;
 #pragma unroll
       for (int m = 0; m < 8; ++m) z[m] = (bf16_t)0.f;
       *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + h * a.o_s1 + 8 * (tid & 15)) = z;
     }
-    return;
   }
-  const int nc = (int)((e - s + C - 1) / C);
-  auto chunk_len = [&](int c) __attribute__((always_inline)) { const int64_t r = e - (s + (int64_t)c * C); return (int)(r < C ? r : C); };
+  int nq = 0;  // chunks in the stream
+  for (int j = 0; j < it.m; ++j) nq += rd32(it.nc, j);
+  if (nq == 0) return;
+  const Pos first = skip_empty(it, Pos{0, 0});
 
-  // Both roles execute exactly 1 + nc workgroup barriers.
+  // Every role executes exactly 1 + nq workgroup barriers.
   if (wave < 4) {
     // ---- state waves: S (K x V fp32) in C layout, m-tile mt = keys 32mt.., this wave's 32 columns
-    const int n = lane & 31, gq = lane >> 5;
-    const int col = 32 * wave + n;
-    float* Sg = a.state + slot * a.st_slot + h * a.st_head;
+    // (lane (n, g) holds column 32 wave + n, keys 32mt + 8 (j / 4) + 4g + j % 4)
     f32x16 S[4];
+    int su = 0;
+    float sb = 0.f;  // upper bound of the column's max |S|, carried across chunks
+    auto state_of = [&](const ChunkAt& ch) __attribute__((always_inline)) {
+      return a.state + (int64_t)ch.slot * a.st_slot + ch.h * a.st_head;
+    };
+    // (the state's lane offsets are recomputed at each load and store rather
+    // than held in registers across the chunk loop)
+    auto load_state = [&](const ChunkAt& ch) __attribute__((always_inline)) {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col];
-    // state units: true state = S * 2^su, with |S| < 2^10 to start with
-    const int sme = col_max_exp(S, 4);
-    int su = sme == kNone ? 0 : sme - 10;
-    float sb = sme == kNone ? 0.f : 1024.f;  // upper bound of the column's max |S|, carried across chunks
-    {
+        for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD];
+      // state units: true state = S * 2^su, with |S| < 2^10 to start with
+      const int sme = col_max_exp(S, 4);
+      su = sme == kNone ? 0 : sme - 10;
+      sb = sme == kNone ? 0.f : 1024.f;
       const float f = __builtin_amdgcn_ldexpf(1.f, -su);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) S[mt][j] *= f;
-    }
+    };
+    Pos p = first;
+    load_state(chunk_at(it, p));
     __syncthreads();  // chunk 0 is prepared
-    for (int c = 0; c < nc; ++c) {
-      consume_chunk<F16>(sm.tiles[c & 1], sm.tb[c % 3], fmaxf(sm.kn2[c % 3][0], sm.kn2[c % 3][1]), sm.v, &sm.v_free, S,
-                    su, sb, a, s + (int64_t)c * C, chunk_len(c), h, wave, lane);
+    for (int q = 0; q < nq; ++q) {
+      const ChunkAt ch = chunk_at(it, p);
+      consume_chunk<F16>(sm.tiles[q & 1], sm.tb[q % 3], fmaxf(sm.kn2[q % 3][0], sm.kn2[q % 3][1]), sm.v, &sm.v_free,
+                         S, su, sb, a, ch.c0, ch.L, ch.h, wave, lane);
       // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
-      if ((c & 15) == 15) sb = col_max(S, 4);
-      __syncthreads();  // chunk c + 1 is prepared
-    }
-    if (__hip_atomic_load(&sm.failed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
-      // a producer wait gave up: NaN in every output row of this item (this
-      // wave's 32 columns), state slot untouched
-      asm volatile("");
-      const s16x4 nan4 = from_f32x4<F16>((f32x4){__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")});
-      const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3], nan4[0], nan4[1], nan4[2], nan4[3]});
-      for (int64_t t = s + (lane >> 2); t < e; t += 16) {
-        *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+      if ((p.c & 15) == 15) sb = col_max(S, 4);
+      const Pos pn = next_pos(it, p);
+      if (pn.j != p.j) {
+        // the item's last chunk: its state goes back to its slot, or, if a
+        // producer wait gave up, NaN in every output row of the item (this
+        // wave's 32 columns) and the slot untouched (the flag stays raised, so
+        // every later item of the workgroup fails the same way)
+        const int64_t s0 = rd64(it.s, p.j);
+        if (__hip_atomic_load(&sm.failed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
+          asm volatile("");
+          const s16x4 nan4 =
+              from_f32x4<F16>((f32x4){__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")});
+          const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3],
+                                                              nan4[0], nan4[1], nan4[2], nan4[3]});
+          for (int64_t t = s0 + (lane >> 2); t < ch.e; t += 16)
+            *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+        } else {
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD] = __builtin_amdgcn_ldexpf(S[mt][j], su);
+        }
+        if (pn.j < it.m) load_state(chunk_at(it, pn));
       }
-      return;
+      p = pn;
+      __syncthreads();  // chunk q + 1 is prepared
     }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        Sg[(32 * mt + 8 * (j >> 2) + 4 * gq + (j & 3)) * VD + col] = __builtin_amdgcn_ldexpf(S[mt][j], su);
     return;
   }
 
-  // ---- producer waves.  While the state waves work on chunk c:
-  //  waves 4 / 5: diagonal block 0 / 1 of T for chunk c + 2;
-  //  wave 6: K tile and decay vectors of chunk c + 1, then A_10 and T_10 of
-  //          chunk c + 1 (its diagonal blocks were solved one iteration earlier);
-  //  wave 7: Q tile and P tiles of chunk c + 1, then its V tile once the
-  //          state waves have released the V tile of chunk c.
+  // ---- producer waves.  While the state waves work on stream chunk q:
+  //  waves 4 / 5: diagonal block 0 / 1 of T for chunk q + 2;
+  //  wave 6: K tile and decay vectors of chunk q + 1, then A_10 and T_10 of
+  //          chunk q + 1 (its diagonal blocks were solved one iteration earlier);
+  //  wave 7: Q tile and P tiles of chunk q + 1, then its V tile once the
+  //          state waves have released the V tile of chunk q.
   // Next-chunk loads go out right after the registers have been staged.
   // A prologue fills the pipeline: diagonal blocks of chunks 0 and 1 and
-  // everything else of chunk 0.
+  // everything else of chunk 0.  Each role keeps its own stream positions.
   const int pw = wave - 4;
-  const ChunkSource src = {&a, a.k + kh * a.k_s1, a.q + kh * a.q_s1, a.v + h * a.v_s1, h, e};
-  auto c0_of = [&](int c) __attribute__((always_inline)) { return s + (int64_t)c * C; };
   if (pw < 2) {
     float* dgam = sm.dvec[pw][0];
     float* dbeta = sm.dvec[pw][1];
     float* deg = sm.dvec[pw][2];
     float* dieg = sm.dvec[pw][3];
     DiagLoad dl;
-    // solve this wave's diagonal block of chunk c (its loads are in dl) into
-    // T buffer c % 3; the loads of chunk c + 1 go out once the fragments are consumed
-    auto solve = [&](int c) __attribute__((always_inline)) {
+    Pos ps = first;  // the chunk whose loads are in dl
+    auto dload = [&](Pos p) __attribute__((always_inline)) {
+      const ChunkAt ch = chunk_at(it, p);
+      load_diag(dl, source_of(a, ch), ch.c0, pw, lane);
+    };
+    // solve this wave's diagonal block of stream chunk q (position ps) into T
+    // buffer q % 3; the loads of the next chunk go out once the fragments are consumed
+    auto solve = [&](int q) __attribute__((always_inline)) {
       float gl;
-      const int L = chunk_len(c);
+      const int L = chunk_at(it, ps).L;
       const float gm = chunk_gamma(dl.d, L, lane, gl);
       dgam[lane] = gm;
       deg[lane] = __expf(gm);
@@ -1196,83 +1303,102 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
 #pragma unroll
         for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(G[j]));
         m = wave_max(m);
-        if (lane == 0) sm.kn2[c % 3][pw] = m;
+        if (lane == 0) sm.kn2[q % 3][pw] = m;
       }
-      if (c + 1 < nc) load_diag(dl, src, c0_of(c + 1), pw, lane);
-      solve_diag_block(sm.tb[c % 3], dgam, dbeta, deg, dieg, fact, G, pw, lane);
+      ps = next_pos(it, ps);
+      if (q + 1 < nq) dload(ps);
+      solve_diag_block(sm.tb[q % 3], dgam, dbeta, deg, dieg, fact, G, pw, lane);
     };
-    load_diag(dl, src, c0_of(0), pw, lane);
+    dload(ps);
     solve(0);
     producer_arrive(&sm.pro, lane);
     producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
-    if (nc > 1) solve(1);
+    if (nq > 1) solve(1);
     __syncthreads();
-    for (int c = 0; c < nc; ++c) {
-      if (c + 2 < nc) solve(c + 2);
+    for (int q = 0; q < nq; ++q) {
+      if (q + 2 < nq) solve(q + 2);
       __syncthreads();
     }
   } else if (pw == 2) {
     TileLoad kl;
     DecayLoad dl;
-    auto load = [&](int c) __attribute__((always_inline)) {
-      const int Lc = chunk_rows(src, c0_of(c));
-      load_tile(kl, src.kg, a.k_s0, c0_of(c), Lc, lane);
-      load_decay(dl, src, c0_of(c), Lc, lane);
+    Pos pl = first;  // the chunk whose loads are in kl / dl
+    auto load = [&]() __attribute__((always_inline)) {
+      const ChunkAt ch = chunk_at(it, pl);
+      const ChunkSource src = source_of(a, ch);
+      const int Lc = chunk_rows(src, ch.c0);
+      load_tile(kl, src.kg, a.k_s0, ch.c0, Lc, lane);
+      load_decay(dl, src, ch.c0, Lc, lane);
     };
-    // K tile and decay vectors of chunk c into tile set c & 1, then release wave 7
-    auto stage = [&](int c) __attribute__((always_inline)) {
-      ChunkTiles& ct = sm.tiles[c & 1];
+    // K tile and decay vectors of stream chunk q into tile set q & 1, then release wave 7
+    auto stage = [&](int q) __attribute__((always_inline)) {
+      ChunkTiles& ct = sm.tiles[q & 1];
       stage_f16<F16>(ct.k, kl, lane);
-      stage_decay(ct, dl, chunk_len(c), a.b_dtype, lane);
+      stage_decay(ct, dl, chunk_at(it, pl).L, a.b_dtype, lane);
       producer_arrive(&sm.kv_ready, lane);
+      pl = next_pos(it, pl);
     };
-    auto offdiag = [&](int c) __attribute__((always_inline)) {
-      b10_block(sm.tiles[c & 1], sm.tb[c % 3], lane);
-      merge_offdiag(sm.tb[c % 3], lane);
+    auto offdiag = [&](int q) __attribute__((always_inline)) {
+      b10_block(sm.tiles[q & 1], sm.tb[q % 3], lane);
+      merge_offdiag(sm.tb[q % 3], lane);
     };
-    load(0);
+    load();
     stage(0);
     producer_arrive(&sm.pro, lane);
     producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
     offdiag(0);
-    if (nc > 1) load(1);
+    if (nq > 1) load();
     __syncthreads();
-    for (int c = 0; c < nc; ++c) {
-      if (c + 1 < nc) {
-        stage(c + 1);
-        if (c + 2 < nc) load(c + 2);
-        offdiag(c + 1);
+    for (int q = 0; q < nq; ++q) {
+      if (q + 1 < nq) {
+        stage(q + 1);
+        if (q + 2 < nq) load();
+        offdiag(q + 1);
       }
       __syncthreads();
     }
   } else {
     TileLoad ql, vl;
-    auto qload = [&](int c) __attribute__((always_inline)) { load_tile(ql, src.qg, a.q_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
-    auto vload = [&](int c) __attribute__((always_inline)) { load_tile(vl, src.vg, a.v_s0, c0_of(c), chunk_rows(src, c0_of(c)), lane); };
-    // Q tile and the three P tiles of chunk c
-    auto qp = [&](int c) __attribute__((always_inline)) {
-      ChunkTiles& ct = sm.tiles[c & 1];
+    Pos pq = first, pv = first;  // the chunks whose loads are in ql / vl
+    auto qload = [&]() __attribute__((always_inline)) {
+      const ChunkAt ch = chunk_at(it, pq);
+      const ChunkSource src = source_of(a, ch);
+      load_tile(ql, src.qg, a.q_s0, ch.c0, chunk_rows(src, ch.c0), lane);
+    };
+    auto vload = [&]() __attribute__((always_inline)) {
+      const ChunkAt ch = chunk_at(it, pv);
+      const ChunkSource src = source_of(a, ch);
+      load_tile(vl, src.vg, a.v_s0, ch.c0, chunk_rows(src, ch.c0), lane);
+    };
+    // Q tile and the three P tiles of stream chunk q
+    auto qp = [&](int q) __attribute__((always_inline)) {
+      ChunkTiles& ct = sm.tiles[q & 1];
       stage_f16<F16>(ct.q, ql, lane);
-      if (c + 1 < nc) qload(c + 1);
-      producer_wait(&sm.kv_ready, c + 1, a.spin_limit, &sm.failed);
+      pq = next_pos(it, pq);
+      if (q + 1 < nq) qload();
+      producer_wait(&sm.kv_ready, q + 1, a.spin_limit, &sm.failed);
       p_tile(ct, 0, 0, lane);
       p_tile(ct, 1, 0, lane);
       p_tile(ct, 1, 1, lane);
     };
-    qload(0);
-    vload(0);
+    auto vstage = [&]() __attribute__((always_inline)) {
+      stage_v(sm.v, vl, lane);
+      pv = next_pos(it, pv);
+    };
+    qload();
+    vload();
     qp(0);
-    stage_v(sm.v, vl, lane);
-    if (nc > 1) vload(1);
+    vstage();
+    if (nq > 1) vload();
     producer_arrive(&sm.pro, lane);
     producer_wait(&sm.pro, 4, a.spin_limit, &sm.failed);
     __syncthreads();
-    for (int c = 0; c < nc; ++c) {
-      if (c + 1 < nc) {
-        qp(c + 1);
-        producer_wait(&sm.v_free, 4 * (c + 1), a.spin_limit, &sm.failed);  // the state waves are done with chunk c's V tile
-        stage_v(sm.v, vl, lane);
-        if (c + 2 < nc) vload(c + 2);
+    for (int q = 0; q < nq; ++q) {
+      if (q + 1 < nq) {
+        qp(q + 1);
+        producer_wait(&sm.v_free, 4 * (q + 1), a.spin_limit, &sm.failed);  // the state waves are done with chunk q's V tile
+        vstage();
+        if (q + 2 < nq) vload();
       }
       __syncthreads();
     }
@@ -1284,7 +1410,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    int32_t spin_limit, hipStream_t st) {
+                                    int32_t spin_limit, int32_t items_per_wg, hipStream_t st) {
   PrefillArgs a;
   a.q = reinterpret_cast<const bf16_t*>(q->data);
   a.k = reinterpret_cast<const bf16_t*>(k->data);
@@ -1314,10 +1440,27 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
   const int64_t nwork = a.nseq * a.Hv;
   if (nwork == 0 || a.T == 0) return hipSuccess;
-  const int64_t nblocks = (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
-  if (q->dtype == GDN_DTYPE_F16)
-    gdn_chunk_prefill_kernel<true><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
-  else
-    gdn_chunk_prefill_kernel<false><<<dim3((unsigned)nblocks), dim3(kThreads), 0, st>>>(a);
+  // Batches of short sequences (at most two chunks on average) with at least
+  // two items per CU: each workgroup walks up to 64 consecutive items as one
+  // chunk stream, so that the next item's pipeline fill overlaps the current
+  // item's chunks.  Otherwise one item per workgroup, longest first.
+  constexpr int64_t kCUs = 256;  // MI355X
+  if (items_per_wg < 0) {
+    const bool short_items = a.T <= 2 * C * a.nseq && nwork >= 2 * kCUs;
+    const int64_t per = (nwork + kCUs - 1) / kCUs;
+    items_per_wg = short_items ? (int32_t)(per < 64 ? per : 64) : 0;
+  }
+  a.per_wg = items_per_wg;
+  const int64_t nblocks = items_per_wg > 0 ? (nwork + items_per_wg - 1) / items_per_wg
+                                           : (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
+  const dim3 grid((unsigned)nblocks), block(kThreads);
+  const bool f16 = q->dtype == GDN_DTYPE_F16;
+  if (items_per_wg > 0) {
+    if (f16) gdn_chunk_prefill_kernel<true, true><<<grid, block, 0, st>>>(a);
+    else gdn_chunk_prefill_kernel<false, true><<<grid, block, 0, st>>>(a);
+  } else {
+    if (f16) gdn_chunk_prefill_kernel<true, false><<<grid, block, 0, st>>>(a);
+    else gdn_chunk_prefill_kernel<false, false><<<grid, block, 0, st>>>(a);
+  }
   return hipGetLastError();
 }

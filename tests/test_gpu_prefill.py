@@ -234,6 +234,57 @@ def test_prefill_fp16_matches_bf16_rounded_inputs(dev):
     torch.testing.assert_close(st_h.cpu(), st_b.cpu(), rtol=1e-5, atol=1e-6)
 
 
+def _stream_batch():
+    """40 sequences of 0..150 tokens with a 0-, 1-, 64-, 65- and 300-token
+    sequence and a padding slot among them (Hk 2 / Hv 4: 160 items)."""
+    gen = torch.Generator().manual_seed(41)
+    lengths = torch.randint(0, 151, (40,), generator=gen).tolist()
+    lengths[3], lengths[5], lengths[9], lengths[10], lengths[11] = 0, 1, 64, 65, 300
+    case = prefill_case(lengths, seed=42, num_slots=48, Hk=2, Hv=4)
+    idx = case.idx.clone()
+    idx[7] = -1
+    return case, idx
+
+
+@pytest.mark.parametrize("per_wg", ["0", "1", "3", "64"])
+def test_prefill_item_stream(dev, monkeypatch, per_wg):
+    """The same batch with one item (sequence, v-head) per workgroup, longest
+    first (0), and with 1, 3 and 64 consecutive items per workgroup walked as
+    one chunk stream, whose producers stage the next item's first chunks while
+    the state waves finish the current item."""
+    case, idx = _stream_batch()
+    monkeypatch.setenv("GDN_PREFILL_ITEMS_PER_WG", per_wg)
+    print(f"prefill item stream: {per_wg} items per workgroup, {case.tokens} tokens", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev, idx=idx)
+    _check(case, o, st, o_ref, st_ref, idx=idx)
+
+
+def test_prefill_many_short_sequences_auto_stream(dev):
+    """600 sequences of 1..128 tokens (2,400 items, under two chunks each on
+    average): the launcher picks the chunk-stream schedule by itself."""
+    gen = torch.Generator().manual_seed(43)
+    lengths = torch.randint(1, 129, (600,), generator=gen).tolist()
+    case = prefill_case(lengths, seed=44, num_slots=640, Hk=2, Hv=4)
+    print(f"prefill many short sequences: {case.tokens} tokens", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_wait_give_up_poisons_the_stream(dev, monkeypatch):
+    """With several items per workgroup a wait that gives up poisons every
+    item of the workgroup from that point: all rows NaN here (the limit is 0
+    from the start), no state slot written."""
+    case, idx = _stream_batch()
+    monkeypatch.setenv("GDN_PREFILL_ITEMS_PER_WG", "8")
+    monkeypatch.setenv("GDN_PREFILL_SPIN_LIMIT", "0")
+    o, st, _, _ = _run(case, dev, idx=idx)
+    pad = torch.zeros(case.tokens, dtype=torch.bool)
+    pad[int(case.cu[7]):int(case.cu[8])] = True
+    assert torch.isnan(o[~pad].float()).all()
+    assert torch.count_nonzero(o[pad]) == 0
+    assert torch.equal(st, case.state)
+
+
 def test_prefill_wait_give_up_poisons_the_item(dev, monkeypatch):
     """The kernel's waits between its wave roles are bounded; one that gives
     up must not pass as a plausible answer.  Forced from the host (spin limit
