@@ -1309,6 +1309,29 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       if (q + 1 < nq) dload(ps);
       solve_diag_block(sm.tb[q % 3], dgam, dbeta, deg, dieg, fact, G, pw, lane);
     };
+    // Several items: the state waves load item j + 1's state right after
+    // storing item j's.  These two waves touch it (one dword per 64 bytes,
+    // half the state each) while the chunk before it runs, so that load finds
+    // it in L2 (a touch two chunks ahead measured slower: the lines are gone
+    // again).  A touch's registers are folded into an accumulator one touch
+    // later, so the wave never waits for one.
+    Pos pp = first;  // stream chunk q + 1
+    uint32_t pacc = 0, pv[8] = {};
+    if constexpr (MULTI)
+      if (pp.j < it.m) pp = next_pos(it, pp);
+    auto touch = [&]() __attribute__((always_inline)) {
+      if (pp.j < it.m && pp.c == 0) {
+        const ChunkAt ch = chunk_at(it, pp);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.state + (int64_t)ch.slot * a.st_slot +
+                                                                ch.h * a.st_head) + pw * (KD * VD / 2) + 16 * lane;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pacc |= pv[i];
+          pv[i] = src[1024 * i];
+        }
+      }
+      if (pp.j < it.m) pp = next_pos(it, pp);
+    };
     dload(ps);
     solve(0);
     producer_arrive(&sm.pro, lane);
@@ -1316,8 +1339,14 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     if (nq > 1) solve(1);
     __syncthreads();
     for (int q = 0; q < nq; ++q) {
+      if constexpr (MULTI) touch();
       if (q + 2 < nq) solve(q + 2);
       __syncthreads();
+    }
+    if constexpr (MULTI) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pacc |= pv[i];
+      asm volatile("" ::"v"(pacc));
     }
   } else if (pw == 2) {
     TileLoad kl;
