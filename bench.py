@@ -50,12 +50,14 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # HBM bytes per launch of each kernel on this benchmark's workloads, from
 # rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch), each
 # scaled by what the same counter reads on a plain 1 GiB streaming copy
-# (--workload hbm_copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0 on MI355X).  Values
-# from the committed profiles of the current kernels (profiles/*.md, which
-# give the commands); a kernel without an entry reports None.
+# (--workload hbm_copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0 on MI355X; the
+# factor 2 is exact for 128-byte read requests, which FETCH_SIZE counts as 64
+# bytes here, and the request-size counters show these kernels issue almost
+# nothing else).  Values from the committed profiles of the current kernels
+# (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_025_893_376,
-    "gdn_chunk_prefill_kernel/short": 3_020_943_155,
+    "gdn_chunk_prefill_kernel": 1_026_671_584,
+    "gdn_chunk_prefill_kernel/short": 3_975_275_424,
     "gdn_recurrent_step_kernel": 1_083_199_150,
     "causal_conv1d_varlen_kernel": 665_974_958,
     "causal_conv1d_step_kernel": 59_313_861,
