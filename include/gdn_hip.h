@@ -243,6 +243,8 @@ int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, const gdn_t
  *   block block_tables[n][j / page].  A query with no visible key gives a
  *   zero row; table entries outside [0, num_blocks) read as zero keys (never
  *   out of bounds).  The reference's block_m_indices work list is not needed.
+ *   GDN_ERR_RANGE when one page of one kv head spans 2^31 bytes or more, or
+ *   max_blocks * page >= 2^31.
  */
 int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn_tensor* v_cache,
                             const gdn_tensor* block_tables, const gdn_tensor* context_lens,

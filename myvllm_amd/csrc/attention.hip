@@ -198,15 +198,73 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.v.base + s0 * a.v.st + kvh * a.v.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.v.st), 0x00020000);
   constexpr int NG = BN / 16;  // 16-row groups of a tile
+  static_assert(CH >= 8 && 64 % CH == 0, "a wave's rows of a tile lie in one 16-row group");
+  // PG == 2: each 16-row group of a tile lies in one page.  Its block id is a
+  // vector load issued one tile ahead, before the previous tile's data loads,
+  // so waiting for it leaves those data loads in flight (a scalar load would
+  // be waited for at once, its value forming the addresses, and that wait
+  // also drains every LDS access in flight).  The rows then load through a
+  // buffer descriptor of the kv head's rows of the page: 32-bit offsets, rows
+  // past the range or of an invalid block read zero.
+  // The 16-row groups are enumerated in order (load_ids runs for tiles 0, 1,
+  // 2, ...), so a group's table column and first page slot are counted up,
+  // not divided out.
+  // An id is kept as the two raw 32-bit words it was loaded as (an int32
+  // table: the entry twice) and decoded only where it is used: converting it
+  // at the load would wait for the load, and with it for every load in flight.
+  uint32_t idlo[NG], idhi[NG];  // raw block ids of the next tile to load
+  bool idin[NG];                // its groups lie inside the range and the table
+  uint32_t slots[NG];           // their first page slot
+  const uint32_t gpp = PG == 2 ? (uint32_t)a.tab.page / 16 : 1u;  // 16-row groups per page
+  uint32_t gcol = 0, grem = 0;  // table column and group within the page of the next group
+  auto load_ids = [&](int t, uint32_t* lo, uint32_t* hi, bool* in, uint32_t* sl) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t j0 = (uint32_t)t * BN + 16 * g;
+      in[g] = j0 < kend && gcol < a.tab.cols;
+      // (the index goes through a vector register so the loads stay vector loads)
+      int64_t e = in[g] ? n * a.tab.row_stride + gcol : 0;
+      asm volatile("" : "+v"(e));
+      const uint32_t* tp = reinterpret_cast<const uint32_t*>(a.tab.table);
+      lo[g] = hi[g] = 0u;
+      if (a.tab.cols > 0) {
+        lo[g] = tp[a.tab.is64 ? 2 * e : e];
+        hi[g] = tp[a.tab.is64 ? 2 * e + 1 : e];
+      }
+      sl[g] = 16 * grem;
+      if (++grem == gpp) {
+        grem = 0;
+        ++gcol;
+      }
+    }
+  };
+  if (PG == 2) load_ids(0, idlo, idhi, idin, slots);
+  const uint32_t kpage = PG == 2 ? (uint32_t)(a.tab.page * a.k.st) : 0u;
+  const uint32_t vpage = PG == 2 ? (uint32_t)(a.tab.page * a.v.st) : 0u;
+  const char* kbase = a.k.base + kvh * a.k.sh;
+  const char* vbase = a.v.base + kvh * a.v.sh;
   auto load_tile = [&](int t, uint4* kd, uint4* vd) {
-    int64_t bl[NG];
+    __amdgpu_buffer_rsrc_t rkg[NG], rvg[NG];
+    uint32_t r0[NG];
     if (PG == 2) {
+      uint32_t nlo[NG], nhi[NG], nsl[NG];
+      bool nin[NG];
+      load_ids(t + 1, nlo, nhi, nin, nsl);
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
-        const int64_t j0 = (int64_t)t * BN + 16 * g, col = j0 / a.tab.page;
-        int64_t blk = -1;
-        if (j0 < kend && col < a.tab.cols) blk = load_index_scalar(a.tab.table, n * a.tab.row_stride + col, a.tab.is64);
-        bl[g] = blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
+        // valid: inside the range, high word zero (int64) or non-negative (int32), below num_blocks
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)idlo[g]);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)idhi[g]);
+        const bool valid = idin[g] && (a.tab.is64 ? hi == 0u : true) && (int64_t)lo < a.tab.num_blocks &&
+                           (a.tab.is64 || (int32_t)lo >= 0);
+        const int64_t bb = valid ? (int64_t)lo : 0;
+        r0[g] = slots[g];
+        rkg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * a.k.sb), 0, valid ? kpage : 0u, 0x00020000);
+        rvg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * a.v.sb), 0, valid ? vpage : 0u, 0x00020000);
+        idlo[g] = nlo[g];
+        idhi[g] = nhi[g];
+        idin[g] = nin[g];
+        slots[g] = nsl[g];
       }
     }
 #pragma unroll
@@ -214,15 +272,30 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       const int c = tid + 256 * i, row = c / CH, ch = c % CH;
       const int64_t j = (int64_t)t * BN + row;
       if (PG == 2) {
-        int64_t blk = bl[0];
+        // the row's 16-row group: i * rows-per-pass / 16 when a pass covers at
+        // most 16 rows (a constant), else plus the wave's part (uniform)
+        constexpr int RPI = 256 / CH;
+        __amdgpu_buffer_rsrc_t rkx, rvx;
+        uint32_t rx;
+        if constexpr (RPI <= 16) {
+          rkx = rkg[i * RPI / 16];
+          rvx = rvg[i * RPI / 16];
+          rx = r0[i * RPI / 16];
+        } else {
+          const int gu = __builtin_amdgcn_readfirstlane(row >> 4);
+          rkx = rkg[0], rvx = rvg[0], rx = r0[0];
 #pragma unroll
-        for (int g = 1; g < NG; ++g) blk = (row >> 4) == g ? bl[g] : blk;
-        const bool ok = j < kend && blk >= 0;
-        const int64_t slot = j % a.tab.page;
-        const char* pk = a.k.base + (ok ? blk * a.k.sb + slot * a.k.st + kvh * a.k.sh : 0);
-        const char* pv = a.v.base + (ok ? blk * a.v.sb + slot * a.v.st + kvh * a.v.sh : 0);
-        kd[i] = ok ? *reinterpret_cast<const uint4*>(pk + 16 * ch) : uint4{0, 0, 0, 0};
-        vd[i] = ok ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+          for (int g = 1; g < NG; ++g) {
+            rkx = gu == g ? rkg[g] : rkx;
+            rvx = gu == g ? rvg[g] : rvx;
+            rx = gu == g ? r0[g] : rx;
+          }
+        }
+        const uint32_t slot = rx + (uint32_t)(row & 15);
+        const uint32_t ko = j < kend ? slot * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
+        const uint32_t vo = j < kend ? slot * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
+        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rkx, ko, 0, 0));
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvx, vo, 0, 0));
         continue;
       }
       if (!PAGED) {

@@ -479,6 +479,12 @@ GDN_EXPORT int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_
   const int64_t R = q->shape[1] / k_cache->shape[2];
   const int64_t gh = R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1);
   if (N > kMaxGridYZ || q->shape[1] / gh > kMaxGridYZ || max_seqlen / 32 > kMaxGrid) return GDN_ERR_RANGE;
+  // one page of one kv head is addressed with 32-bit byte offsets below 2^31,
+  // key positions (at most columns x page) with 32-bit integers
+  const int64_t es = elem_size(k_cache->dtype);
+  if (k_cache->shape[1] * std::max(k_cache->stride[1], v_cache->stride[1]) * es >= (int64_t(1) << 31) ||
+      block_tables->shape[1] * k_cache->shape[1] >= (int64_t(1) << 31))
+    return GDN_ERR_RANGE;
   return launch_rc(attn_paged_prefill_launch(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens, out,
                                              max_seqlen, scale, reinterpret_cast<hipStream_t>(stream)));
 }

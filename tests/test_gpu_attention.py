@@ -14,7 +14,8 @@ import torch
 
 from conftest import assert_out_close
 from myvllm_amd import flash_attention_prefill, paged_flash_attention_decode, paged_flash_attention_prefill
-from myvllm_amd.workloads import attn_decode_case, attn_prefill_32k_case, attn_varlen_case, paged_case
+from myvllm_amd.workloads import (attn_decode_case, attn_paged_prefill_case, attn_prefill_32k_case, attn_varlen_case,
+                                   paged_case)
 from oracle.attention import attention_rows_ref, flash_attention_prefill_ref, gather_paged, paged_attention_ref
 
 pytestmark = pytest.mark.gpu
@@ -88,6 +89,9 @@ def test_varlen_prefill_layer_workload_sampled_rows(dev):
         ([40, 300, 17], [40, 100, 1], 16, 16, 2, 256),  # no prefix / prefix / one new token
         ([77, 130], [33, 130], 7, 4, 4, 128),  # page size 7, MHA
         ([64, 0, 5], [10, 0, 5], 16, 8, 2, 64),  # an empty sequence
+        ([200, 1000], [200, 300], 32, 16, 2, 256),  # a page holds a whole 32-key tile
+        ([300, 513], [100, 513], 48, 8, 2, 128),  # page 48: tiles of 64 keys straddle pages
+        ([129, 64], [65, 64], 16, 8, 8, 128),  # four 16-row groups per 64-key tile
     ],
 )
 def test_paged_prefill(dev, ctx, new, page, Hq, Hkv, Dh):
@@ -99,6 +103,38 @@ def test_paged_prefill(dev, ctx, new, page, Hq, Hkv, Dh):
     ref = paged_attention_ref(case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens, case.cu,
                               case.scale)
     assert_attn_close(out, ref)
+
+
+def test_paged_prefill_int64_table(dev):
+    case = paged_case([300, 77], [150, 77], page=16, seed=11, Hq=16, Hkv=2, D=256)
+    tab = case.block_tables.to(torch.int64)
+    print("paged prefill int64 block table", flush=True)
+    out = paged_flash_attention_prefill(case.q.to(dev), case.k_cache.to(dev), case.v_cache.to(dev), tab.to(dev),
+                                        case.context_lens.to(dev), case.cu.to(dev), None, case.scale, 16).cpu()
+    ref = paged_attention_ref(case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens, case.cu,
+                              case.scale)
+    assert_attn_close(out, ref)
+
+
+def test_paged_prefill_workload_sampled_rows(dev):
+    """The chunked-prefill workload over the paged cache (16 sequences, cached
+    prefixes U[0, 4096], new chunks U[256, 2048], 16-token pages, Hq 16, Hkv 2,
+    D 256): every sequence's first, last and 14 random new rows vs the oracle."""
+    case = attn_paged_prefill_case()
+    print(f"paged prefill workload T={case.q.shape[0]}", flush=True)
+    out = paged_flash_attention_prefill(case.q.to(dev), case.k_cache.to(dev), case.v_cache.to(dev),
+                                        case.block_tables.to(dev), case.context_lens.to(dev), case.cu.to(dev),
+                                        None, case.scale, case.page, max_seqlen=case.max_len).cpu()
+    g = torch.Generator().manual_seed(8)
+    cu = case.cu.tolist()
+    for n in range(len(cu) - 1):
+        s, e = cu[n], cu[n + 1]
+        L = int(case.context_lens[n])
+        k = gather_paged(case.k_cache, case.block_tables[n], L)
+        v = gather_paged(case.v_cache, case.block_tables[n], L)
+        rows = torch.cat([torch.tensor([0, e - s - 1]), torch.randint(0, e - s, (14,), generator=g)])
+        ref = attention_rows_ref(case.q[s + rows], k, v, rows + (L - (e - s)), case.scale, causal=True)
+        assert_attn_close(out[s + rows], ref)
 
 
 def _decode(case, dev, splits):
