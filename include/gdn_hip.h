@@ -114,8 +114,10 @@ int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tenso
  *   state_indices : (N,) i32|i64
  *   cu_seqlens    : (N+1,) i32|i64
  *   out    : (T, Hv, V)  v's dtype, last stride 1
- * chunk_size must be 64; K = V = 128.  Tokens not covered by any sequence
- * keep whatever `out` held.
+ * chunk_size must be 64; K and V multiples of 8 from 8 to 128 (the
+ * reference's k_head_dim <= 128, ops/gated_delta_rule/h.py:211; head dims
+ * below 128 run zero-padded to 128, at the cost of 128).  Tokens not covered
+ * by any sequence keep whatever `out` held.
  * Range: the MFMA operands are fp16, so every q and k row must have an L2
  * norm of at most 128 (the layer's rows are L2-normalised, norm 1) and |v|
  * entries must stay below 65504 (an fp16 out also overflows past 65504, as

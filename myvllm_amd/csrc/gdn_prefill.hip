@@ -82,6 +82,7 @@ struct PrefillArgs {
   float scale;
   int32_t spin_limit;  // bound of a producer wait (sleep iterations)
   int32_t per_wg;      // items per workgroup: 0 = one item, longest first; else consecutive work ids
+  int32_t kd, vd;      // key and value head dims (multiples of 8 up to 128; smaller ones run zero-padded)
   bool idx64, cu64;
 };
 
@@ -518,10 +519,14 @@ GDN_DEVICE bf16x8 load_row_piece(const bf16_t* chunk_base, uint32_t stride, int 
 struct TileLoad {
   bf16x8 r[16];
 };
-GDN_DEVICE void load_tile(TileLoad& tl, const bf16_t* head_base, int64_t stride, int64_t c0, int Lc, int lane) {
+// With a head dim below 128 (dim), a lane whose columns lie past it reads
+// column 0 instead (in bounds); staging zeroes them.
+GDN_DEVICE void load_tile(TileLoad& tl, const bf16_t* head_base, int64_t stride, int64_t c0, int Lc, int lane,
+                          int dim = KD) {
   const bf16_t* b = head_base + c0 * stride;
+  const int col = 8 * (lane & 15) < dim ? 8 * (lane & 15) : 0;
 #pragma unroll
-  for (int u = 0; u < 16; ++u) tl.r[u] = load_row_piece(b, (uint32_t)stride, (lane >> 4) + 4 * u, 8 * (lane & 15), Lc);
+  for (int u = 0; u < 16; ++u) tl.r[u] = load_row_piece(b, (uint32_t)stride, (lane >> 4) + 4 * u, col, Lc);
 }
 
 // g and beta (raw bits) of token `lane` of a chunk.
@@ -542,13 +547,15 @@ struct DiagLoad {
   bf16x8 kf[8];
   DecayLoad d;
 };
-GDN_DEVICE void load_diag(DiagLoad& dl, const ChunkSource& src, int64_t c0, int blk, int lane) {
+GDN_DEVICE void load_diag(DiagLoad& dl, const ChunkSource& src, int64_t c0, int blk, int lane, int dim = KD) {
   const PrefillArgs& a = *src.a;
   const int Lc = chunk_rows(src, c0);
   const bf16_t* kb = src.kg + c0 * a.k_s0;
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks)
-    dl.kf[ks] = load_row_piece(kb, (uint32_t)a.k_s0, 32 * blk + (lane & 31), 16 * ks + 8 * (lane >> 5), Lc);
+  for (int ks = 0; ks < 8; ++ks) {
+    const int col = 16 * ks + 8 * (lane >> 5);
+    dl.kf[ks] = load_row_piece(kb, (uint32_t)a.k_s0, 32 * blk + (lane & 31), col < dim ? col : 0, Lc);
+  }
   load_decay(dl.d, src, c0, Lc, lane);
 }
 
@@ -822,22 +829,23 @@ GDN_DEVICE void p_tile(ChunkTiles& ct, int mt, int nt, int lane) {
 // Stage a tile held in registers into LDS (fp16 for K/Q, the raw 16-bit
 // elements for V).
 template <bool F16>
-GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane) {
+GDN_DEVICE void stage_f16(f16_t* dst, const TileLoad& tl, int lane, bool keep = true) {
   // lane's 8 logical columns 8a..8a+7 (a = lane % 16) are quads 2a', 2a'+1 of
   // 16-column group a / 2 (a' = a % 2), stored at quads kq_quad(2a'), kq_quad(2a'+1)
   const int a = lane & 15, grp = 16 * (a >> 1), q0 = 2 * (a & 1);
   const int off0 = grp + 4 * kq_quad(q0), off1 = grp + 4 * kq_quad(q0 + 1);
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
-    const f16x8 v = to_f16x8<F16>(tl.r[u]);
+    const f16x8 v = keep ? to_f16x8<F16>(tl.r[u]) : f16x8{};  // (keep: the lane's columns lie inside the head dim)
     f16_t* row = dst + ((lane >> 4) + 4 * u) * LDK;
     *reinterpret_cast<f16x4*>(row + off0) = (f16x4){v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f16x4*>(row + off1) = (f16x4){v[4], v[5], v[6], v[7]};
   }
 }
-GDN_DEVICE void stage_v(bf16_t* dst, const TileLoad& tl, int lane) {
+GDN_DEVICE void stage_v(bf16_t* dst, const TileLoad& tl, int lane, bool keep = true) {
 #pragma unroll
-  for (int u = 0; u < 16; ++u) *reinterpret_cast<bf16x8*>(dst + ((lane >> 4) + 4 * u) * LDV + 8 * (lane & 15)) = tl.r[u];
+  for (int u = 0; u < 16; ++u)
+    *reinterpret_cast<bf16x8*>(dst + ((lane >> 4) + 4 * u) * LDV + 8 * (lane & 15)) = keep ? tl.r[u] : bf16x8{};
 }
 
 // Decay vectors of a chunk for the state waves and the producers' epilogues.
@@ -872,7 +880,7 @@ GDN_DEVICE int out_slot(int s, int m) {
 // mixes value columns): the update rescales S by one factor per chunk and
 // picks the new units from the exponents of V' and of the decayed state, so
 // S stays below 2^14 and is split without another pass over it.
-template <bool F16>
+template <bool F16, bool PAD>
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, bf16_t* vt, int32_t* v_free,
                               f32x16 (&S)[4], int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h,
                               int wave, int lane) {
@@ -997,7 +1005,7 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
         half[hh] = tr_read(vt + (2 * m + (u >> 1)) * LDV + 32 * wave + 4 * out_slot(4 * (u & 1) + (j & 3), m));
       }
       const int row = 16 * u + j;
-      if (row < L)
+      if (row < L && (!PAD || 32 * wave + 8 * qd < a.vd))
         *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(ob) + (uint32_t)row * (uint32_t)a.o_s0 * 2u) =
             __builtin_bit_cast(u32x4, (s16x8){half[0][0], half[0][1], half[0][2], half[0][3],
                                                half[1][0], half[1][1], half[1][2], half[1][3]});
@@ -1142,7 +1150,9 @@ GDN_DEVICE void item_fields(const PrefillArgs& a, int64_t seq, int h, Items& it)
 // MULTI: several items per workgroup (a.per_wg > 0); the one-item schedule
 // is its own instantiation, so the long-sequence path pays nothing for the
 // item stream.
-template <bool F16, bool MULTI>
+// PAD: head dims below 128, zero-padded to 128 in the tiles and the state
+// registers (zero key columns and zero value columns leave the rest exact).
+template <bool F16, bool MULTI, bool PAD>
 __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
   __shared__ Smem sm;
 
@@ -1180,6 +1190,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     if (rd32(it.slot, j) >= 0) continue;
     const int64_t s = rd64(it.s, j), e = rd64(it.e, j);
     const int h = rd32(it.h, j);
+    if (PAD && 8 * (tid & 15) >= a.vd) continue;  // (no barrier or cross-lane step follows in this loop)
     for (int64_t t = s + (tid >> 4); t < e; t += kThreads / 16) {
       bf16x8 z;
 #pragma unroll
@@ -1207,11 +1218,26 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     auto load_state = [&](const ChunkAt& ch) __attribute__((always_inline)) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
-      const float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+      if constexpr (PAD) {
+        // rows of a.vd values; keys past a.kd and values past a.vd are zero
+        const float* Sb = state_of(ch);
+        const int c = 32 * wave + (ln & 31);
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD];
+          for (int j = 0; j < 16; ++j) {
+            const int r = 32 * mt + 8 * (j >> 2) + (j & 3) + 4 * (ln >> 5);
+            const bool in = r < a.kd && c < a.vd;
+            const float x = Sb[in ? r * a.vd + c : 0];
+            S[mt][j] = in ? x : 0.f;
+          }
+      } else {
+        const float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) S[mt][j] = Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD];
+      }
       // state units: true state = S * 2^su, with |S| < 2^10 to start with
       const int sme = col_max_exp(S, 4);
       su = sme == kNone ? 0 : sme - 10;
@@ -1227,7 +1253,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     __syncthreads();  // chunk 0 is prepared
     for (int q = 0; q < nq; ++q) {
       const ChunkAt ch = chunk_at(it, p);
-      consume_chunk<F16>(sm.tiles[q & 1], sm.tb[q % 3], fmaxf(sm.kn2[q % 3][0], sm.kn2[q % 3][1]), sm.v, &sm.v_free,
+      consume_chunk<F16, PAD>(sm.tiles[q & 1], sm.tb[q % 3], fmaxf(sm.kn2[q % 3][0], sm.kn2[q % 3][1]), sm.v, &sm.v_free,
                          S, su, sb, a, ch.c0, ch.L, ch.h, wave, lane);
       // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
       if ((p.c & 15) == 15) sb = col_max(S, 4);
@@ -1244,17 +1270,30 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
               from_f32x4<F16>((f32x4){__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")});
           const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3],
                                                               nan4[0], nan4[1], nan4[2], nan4[3]});
-          for (int64_t t = s0 + (lane >> 2); t < ch.e; t += 16)
-            *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+          if (!PAD || 32 * wave + 8 * (lane & 3) < a.vd)
+            for (int64_t t = s0 + (lane >> 2); t < ch.e; t += 16)
+              *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
         } else {
           int ln = lane;
           asm volatile("" : "+v"(ln));
-          float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+          if constexpr (PAD) {
+            float* Sb = state_of(ch);
+            const int c = 32 * wave + (ln & 31);
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
+            for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-              Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD] = __builtin_amdgcn_ldexpf(S[mt][j], su);
+              for (int j = 0; j < 16; ++j) {
+                const int r = 32 * mt + 8 * (j >> 2) + (j & 3) + 4 * (ln >> 5);
+                if (r < a.kd && c < a.vd) Sb[r * a.vd + c] = __builtin_amdgcn_ldexpf(S[mt][j], su);
+              }
+          } else {
+            float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+              for (int j = 0; j < 16; ++j)
+                Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD] = __builtin_amdgcn_ldexpf(S[mt][j], su);
+          }
         }
         if (pn.j < it.m) load_state(chunk_at(it, pn));
       }
@@ -1283,7 +1322,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     Pos ps = first;  // the chunk whose loads are in dl
     auto dload = [&](Pos p) __attribute__((always_inline)) {
       const ChunkAt ch = chunk_at(it, p);
-      load_diag(dl, source_of(a, ch), ch.c0, pw, lane);
+      load_diag(dl, source_of(a, ch), ch.c0, pw, lane, PAD ? a.kd : KD);
     };
     // solve this wave's diagonal block of stream chunk q (position ps) into T
     // buffer q % 3; the loads of the next chunk go out once the fragments are consumed
@@ -1296,6 +1335,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       dieg[lane] = __expf(-gm);
       const bool fact = factorable(gm);
       dbeta[lane] = lane < L ? scalar_raw_f32(dl.d.b, a.b_dtype) : 0.f;
+      if constexpr (PAD) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+          if (16 * ks + 8 * (lane >> 5) >= a.kd) dl.kf[ks] = bf16x8{};
+      }
       const f32x16 G = gram_regs<F16>(dl.kf);
       // max_i |k_i|^2 over this block's rows: the largest |k_i.k_j| of the Gram (Cauchy-Schwarz)
       {
@@ -1319,7 +1363,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     // touch later, so the wave never waits for one.
     Pos pp = first;  // stream chunk q + 1
     uint32_t pacc = 0, pv[8] = {};
-    if constexpr (MULTI)
+    if constexpr (MULTI && !PAD)
       if (pp.j < it.m) pp = next_pos(it, pp);
     auto touch = [&]() __attribute__((always_inline)) {
       if (pp.j < it.m && pp.c == 0) {
@@ -1342,10 +1386,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     __syncthreads();
     for (int q = 0; q < nq; ++q) {
       if (q + 2 < nq) solve(q + 2);
-      if constexpr (MULTI) touch();
+      if constexpr (MULTI && !PAD) touch();
       __syncthreads();
     }
-    if constexpr (MULTI) {
+    if constexpr (MULTI && !PAD) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) pacc |= pv[i];
       asm volatile("" ::"v"(pacc));
@@ -1358,13 +1402,13 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       const ChunkAt ch = chunk_at(it, pl);
       const ChunkSource src = source_of(a, ch);
       const int Lc = chunk_rows(src, ch.c0);
-      load_tile(kl, src.kg, a.k_s0, ch.c0, Lc, lane);
+      load_tile(kl, src.kg, a.k_s0, ch.c0, Lc, lane, PAD ? a.kd : KD);
       load_decay(dl, src, ch.c0, Lc, lane);
     };
     // K tile and decay vectors of stream chunk q into tile set q & 1, then release wave 7
     auto stage = [&](int q) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[q & 1];
-      stage_f16<F16>(ct.k, kl, lane);
+      stage_f16<F16>(ct.k, kl, lane, !PAD || 8 * (lane & 15) < a.kd);
       stage_decay(ct, dl, chunk_at(it, pl).L, a.b_dtype, lane);
       producer_arrive(&sm.kv_ready, lane);
       pl = next_pos(it, pl);
@@ -1394,17 +1438,17 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     auto qload = [&]() __attribute__((always_inline)) {
       const ChunkAt ch = chunk_at(it, pq);
       const ChunkSource src = source_of(a, ch);
-      load_tile(ql, src.qg, a.q_s0, ch.c0, chunk_rows(src, ch.c0), lane);
+      load_tile(ql, src.qg, a.q_s0, ch.c0, chunk_rows(src, ch.c0), lane, PAD ? a.kd : KD);
     };
     auto vload = [&]() __attribute__((always_inline)) {
       const ChunkAt ch = chunk_at(it, pv);
       const ChunkSource src = source_of(a, ch);
-      load_tile(vl, src.vg, a.v_s0, ch.c0, chunk_rows(src, ch.c0), lane);
+      load_tile(vl, src.vg, a.v_s0, ch.c0, chunk_rows(src, ch.c0), lane, PAD ? a.vd : VD);
     };
     // Q tile and the three P tiles of stream chunk q
     auto qp = [&](int q) __attribute__((always_inline)) {
       ChunkTiles& ct = sm.tiles[q & 1];
-      stage_f16<F16>(ct.q, ql, lane);
+      stage_f16<F16>(ct.q, ql, lane, !PAD || 8 * (lane & 15) < a.kd);
       pq = next_pos(it, pq);
       if (q + 1 < nq) qload();
       producer_wait(&sm.kv_ready, q + 1, a.spin_limit, &sm.failed);
@@ -1413,7 +1457,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
       p_tile(ct, 1, 1, lane);
     };
     auto vstage = [&]() __attribute__((always_inline)) {
-      stage_v(sm.v, vl, lane);
+      stage_v(sm.v, vl, lane, !PAD || 8 * (lane & 15) < a.vd);
       pv = next_pos(it, pv);
     };
     qload();
@@ -1469,6 +1513,8 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   a.spin_limit = spin_limit;
   a.idx64 = idx->dtype == GDN_DTYPE_I64;
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
+  a.kd = (int32_t)q->shape[2];
+  a.vd = (int32_t)v->shape[2];
   const int64_t nwork = a.nseq * a.Hv;
   if (nwork == 0 || a.T == 0) return hipSuccess;
   // Batches of short sequences (at most two chunks on average) with at least
@@ -1485,13 +1531,23 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   const int64_t nblocks = items_per_wg > 0 ? (nwork + items_per_wg - 1) / items_per_wg
                                            : (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
   const dim3 grid((unsigned)nblocks), block(kThreads);
-  const bool f16 = q->dtype == GDN_DTYPE_F16;
-  if (items_per_wg > 0) {
-    if (f16) gdn_chunk_prefill_kernel<true, true><<<grid, block, 0, st>>>(a);
-    else gdn_chunk_prefill_kernel<false, true><<<grid, block, 0, st>>>(a);
+  const bool f16 = q->dtype == GDN_DTYPE_F16, multi = items_per_wg > 0;
+  if (a.kd == KD && a.vd == VD) {
+    if (multi) {
+      if (f16) gdn_chunk_prefill_kernel<true, true, false><<<grid, block, 0, st>>>(a);
+      else gdn_chunk_prefill_kernel<false, true, false><<<grid, block, 0, st>>>(a);
+    } else {
+      if (f16) gdn_chunk_prefill_kernel<true, false, false><<<grid, block, 0, st>>>(a);
+      else gdn_chunk_prefill_kernel<false, false, false><<<grid, block, 0, st>>>(a);
+    }
   } else {
-    if (f16) gdn_chunk_prefill_kernel<true, false><<<grid, block, 0, st>>>(a);
-    else gdn_chunk_prefill_kernel<false, false><<<grid, block, 0, st>>>(a);
+    if (multi) {
+      if (f16) gdn_chunk_prefill_kernel<true, true, true><<<grid, block, 0, st>>>(a);
+      else gdn_chunk_prefill_kernel<false, true, true><<<grid, block, 0, st>>>(a);
+    } else {
+      if (f16) gdn_chunk_prefill_kernel<true, false, true><<<grid, block, 0, st>>>(a);
+      else gdn_chunk_prefill_kernel<false, false, true><<<grid, block, 0, st>>>(a);
+    }
   }
   return hipGetLastError();
 }

@@ -70,15 +70,17 @@ def prefill_case(
     g_scale: float = 1.0,
     beta_dtype: torch.dtype = torch.float32,
     dtype: torch.dtype = torch.bfloat16,
+    K: int = DK,
+    V: int = DV,
 ) -> PrefillCase:
     """Chunked-prefill inputs for given sequence lengths (draws after the lengths)."""
     gen = torch.Generator().manual_seed(seed)
     N = len(lengths)
     cu = cu_from_lengths(lengths)
     T = int(cu[-1])
-    q, k, v, g, beta = gdn_inputs(gen, T, Hk, Hv, dtype=dtype, beta_dtype=beta_dtype, g_scale=g_scale)
+    q, k, v, g, beta = gdn_inputs(gen, T, Hk, Hv, K=K, V=V, dtype=dtype, beta_dtype=beta_dtype, g_scale=g_scale)
     num_slots = num_slots or max(N, 1)
-    state = torch.randn(num_slots, Hv, DK, DV, generator=gen) * state_std
+    state = torch.randn(num_slots, Hv, K, V, generator=gen) * state_std
     idx = torch.randperm(num_slots, generator=gen)[:N].to(torch.int32)
     return PrefillCase(q, k, v, g, beta, state, idx, cu)
 

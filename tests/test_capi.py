@@ -114,9 +114,10 @@ def test_prefill_validation():
     b = _recurrent_args(B=10, dtype=torch.float32)
     b["idx"] = torch.zeros(2, dtype=torch.int32)
     assert _call_prefill(b, cu) == ERR["DTYPE"]  # prefill takes bf16 or fp16 q/k/v only
-    c = _recurrent_args(B=10, K=64, V=64)
-    c["idx"] = torch.zeros(2, dtype=torch.int32)
-    assert _call_prefill(c, cu) == ERR["HEAD_DIM"]
+    for K, V in ((100, 64), (136, 128), (128, 4), (0, 64)):  # head dims: multiples of 8 in 8..128
+        c = _recurrent_args(B=10, K=K, V=V)
+        c["idx"] = torch.zeros(2, dtype=torch.int32)
+        assert _call_prefill(c, cu) == ERR["HEAD_DIM"], (K, V)
     d = _recurrent_args(B=10)
     d["idx"] = torch.zeros(2, dtype=torch.int32)
     d["g"] = torch.zeros(10, 4, dtype=torch.bfloat16)

@@ -41,6 +41,27 @@ def test_prefill_varlen_edges(dev, lengths):
     _check(case, o, st, o_ref, st_ref)
 
 
+@pytest.mark.parametrize("K, V", [(64, 64), (128, 64), (64, 128), (96, 32), (8, 120)])
+def test_prefill_head_dims(dev, K, V):
+    """Head dims below 128 (multiples of 8) run zero-padded to 128: keys past K
+    and values past V stay zero in the tiles and the state, the rest is exact."""
+    case = prefill_case([200, 1, 65, 130], seed=K + V, num_slots=6, Hk=2, Hv=4, K=K, V=V)
+    print(f"prefill head dims K={K} V={V}", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
+def test_prefill_head_dim_64_item_stream_fp16(dev):
+    """d 64, fp16 q/k/v, 600 short sequences: the several-items-per-workgroup
+    schedule with zero-padded head dims."""
+    g = torch.Generator().manual_seed(21)
+    lengths = torch.randint(1, 100, (600,), generator=g).tolist()
+    case = prefill_case(lengths, seed=22, num_slots=640, Hk=1, Hv=2, K=64, V=64, dtype=torch.float16)
+    print(f"prefill d64 fp16 item stream T={int(case.cu[-1])}", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev)
+    _check(case, o, st, o_ref, st_ref)
+
+
 def test_prefill_gva_ratio_one_and_four(dev):
     for Hk, Hv in ((4, 4), (1, 4)):
         case = prefill_case([70, 33], seed=7, num_slots=4, Hk=Hk, Hv=Hv)
