@@ -138,6 +138,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   static_assert(BN % 32 == 0 && (BN * CH) % 256 == 0, "tile");
   __shared__ __align__(16) T ks[2][BN * LDK];
   __shared__ __align__(16) T vs[2][BN * LDV];
+  // D = 256: each wave's query fragments sit in LDS (16.5 KB per wave)
+  // instead of 64 VGPRs; the registers this frees hold the K, Q and V
+  // fragments of the next MFMAs while the current one runs (with Q resident
+  // the allocator kept one fragment buffer, so every LDS read was waited for
+  // right before its MFMA)
+  constexpr bool QL = D == 256;
+  __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t n = blockIdx.z;
@@ -187,6 +194,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < NKS; ++s) qf[s] = c < 0.f ? -qf[s] : v8{};
     c = c < 0.f ? -c : 1.f;
+  }
+  T* const qw = qs + (QL ? w * 32 * LDK : 0);  // this wave's query rows (only the wave reads them)
+  if constexpr (QL) {
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) *reinterpret_cast<v8*>(qw + col * LDK + 16 * s + 8 * hh) = qf[s];
   }
 
   // staging of a K/V tile: global rows -> registers (rows past kend read as
@@ -335,8 +347,22 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       for (int aa = 0; aa < NA; ++aa) {
         s[aa] = f32x16{};
         const T* kp = K + (32 * aa + col) * LDK + 8 * hh;
+        if constexpr (QL) {
+          const T* qp = qw + col * LDK + 8 * hh;
 #pragma unroll
-        for (int k = 0; k < NKS; ++k) s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), qf[k], s[aa]);
+          for (int k = 0; k < NKS; ++k)
+            s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), *reinterpret_cast<const v8*>(qp + 16 * k), s[aa]);
+          // schedule: the K and Q fragments of the next k-steps are read while each MFMA runs
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+          for (int k = 0; k < NKS; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if (k + 2 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < NKS; ++k) s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), qf[k], s[aa]);
+        }
       }
       // mask keys past the sequence / context and, if causal, past the query
       const int64_t tk0 = (int64_t)t * BN;
@@ -381,12 +407,27 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           // V^T fragment for keys 32 aa + 16 h2 + {4 hh + 0..3, 8 + 4 hh + 0..3}
           const int j16 = lane & 15, qd = lane >> 4;
           const T* vp = V + (32 * aa + 16 * h2 + 4 * (qd >> 1) + (j16 >> 2)) * LDV + 16 * (qd & 1) + 4 * (j16 & 3);
-#pragma unroll
-          for (int d = 0; d < NDT; ++d) {
+          auto vfrag = [&](int d) __attribute__((always_inline)) {
             const v4 lo = tr4<v4>(vp + 32 * d);
             const v4 hi = tr4<v4>(vp + 32 * d + 8 * LDV);
-            const v8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            oacc[d] = M::m32(vf, pf, oacc[d]);
+            return v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          };
+          if constexpr (QL) {
+            // the V fragments of two MFMAs ahead are in flight while each
+            // MFMA runs; the scheduling barrier keeps the reads ahead
+            constexpr int AH = 2;
+            v8 vf[AH + 1];
+#pragma unroll
+            for (int i = 0; i < AH; ++i) vf[i] = vfrag(i);
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) {
+              if (d + AH < NDT) vf[(d + AH) % (AH + 1)] = vfrag(d + AH);
+              __builtin_amdgcn_sched_barrier(0);
+              oacc[d] = M::m32(vf[d % (AH + 1)], pf, oacc[d]);
+            }
+          } else {
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) oacc[d] = M::m32(vfrag(d), pf, oacc[d]);
           }
         }
       }
