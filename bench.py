@@ -56,15 +56,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_026_671_584,
-    "gdn_chunk_prefill_kernel/short": 3_975_275_424,
-    "gdn_recurrent_step_kernel": 1_083_199_150,
-    "causal_conv1d_varlen_kernel": 665_974_958,
-    "causal_conv1d_step_kernel": 59_313_861,
-    "gdn_decode_fused_kernel": 1_131_364_391,
-    "attn_prefill_kernel": 1_327_211_637,
-    "attn_decode_kernel": 1_253_245_959,
-    "attn_paged_prefill_kernel": 1_153_418_650,
+    "gdn_chunk_prefill_kernel": 1_026_612_864,
+    "gdn_chunk_prefill_kernel/short": 3_963_057_648,
+    "gdn_recurrent_step_kernel": 1_083_206_624,
+    "causal_conv1d_varlen_kernel": 665_998_080,
+    "causal_conv1d_step_kernel": 59_315_392,
+    "gdn_decode_fused_kernel": 1_131_404_992,
+    "attn_prefill_kernel": 1_333_052_416,
+    "attn_decode_kernel": 1_269_001_288,  # with its combine kernel
+    "attn_paged_prefill_kernel": 1_185_898_752,
 }
 
 
