@@ -924,9 +924,11 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
       const int j = lane & 15, qd = lane >> 4;
       const bf16_t* p = vt + (32 * mt + 8 * i + 4 * (qd >> 1) + (j >> 2)) * LDV + 32 * wave + 16 * (qd & 1) + 4 * (j & 3);
       const f32x4 vv = to_f32x4<F16>(tr_read(p));
+      // (v - e^gamma 2^su X) first, in one fma, then times beta: one multiply
+      // per element less than scaling both terms by beta, and the cancellation
+      // happens before any rounding
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        X[mt][4 * i + rr] = fmaf(-(egv[rr] * xu * bv[rr]), X[mt][4 * i + rr], vv[rr] * bv[rr]);
+      for (int rr = 0; rr < 4; ++rr) X[mt][4 * i + rr] = bv[rr] * fmaf(-(egv[rr] * xu), X[mt][4 * i + rr], vv[rr]);
     }
   }
   f32x16* R = X;  // X now holds R
