@@ -95,7 +95,8 @@ typedef struct gdn_tensor {
  *   state_indices : (B,) i32|i64
  *   out    : (B, Hv, V)  bf16|f16|f32, last stride 1
  * Per (b, h): S <- e^g S; d = beta (v - S^T k); S += k d^T; o = S^T (scale q).
- * Supported head dims: K = V = 128 or K = V = 64.
+ * Head dims: K and V multiples of 8 up to 128 (64 x 64 and 128 x 128 have
+ * their own kernels; other shapes run zero-padded in the 128 x 128 one).
  */
 int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                        const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,

@@ -140,7 +140,8 @@ int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* 
     // multiples of 8 up to 128 (16-byte rows); below 128 the kernel pads with zeros
     if (K < 8 || K > 128 || K % 8 != 0 || V < 8 || V > 128 || V % 8 != 0) return GDN_ERR_HEAD_DIM;
   } else {
-    if (!((K == 128 && V == 128) || (K == 64 && V == 64))) return GDN_ERR_HEAD_DIM;
+    // multiples of 8 up to 128 (64 x 64 and 128 x 128 have their own kernels, others run zero-padded)
+    if (K < 8 || K > 128 || K % 8 != 0 || V < 8 || V > 128 || V % 8 != 0) return GDN_ERR_HEAD_DIM;
   }
 
   // strides

@@ -29,6 +29,7 @@ struct RecurrentArgs {
   int32_t Hv, r;  // r = Hv / Hk
   int32_t g_dtype, b_dtype;
   float scale;
+  int32_t kd, vd;  // head dims of the PAD instantiation (multiples of 8 up to its K, V)
   bool idx64;
 };
 
@@ -36,7 +37,11 @@ struct RecurrentArgs {
 // (measured against 256 / 512 threads and two heads per workgroup).
 constexpr int kThreads = 1024;
 
-template <typename TIn, int K, int V, int NH>
+// PAD: head dims a.kd <= K, a.vd <= V (multiples of 8) run in the K x V
+// instantiation: state rows past kd and column groups past vd are neither
+// loaded (zero) nor stored, q/k/v past the dims read as zero, and output
+// columns past vd are not written; the state's rows are vd floats long.
+template <typename TIn, int K, int V, int NH, bool PAD = false>
 __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentArgs a) {
   constexpr int CG = V / 4;           // float4 column groups per row
   constexpr int RG = kThreads / CG;   // row groups
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
   if (slot < 0 || slot >= a.num_slots) {  // padding sequence: zero output, state untouched
 #pragma unroll
     for (int n = 0; n < NH; ++n)
-      if (tid < V) reinterpret_cast<TIn*>(a.out)[b * a.o_s0 + (h0 + n) * a.o_s1 + tid] = from_f32<TIn>(0.0f);
+      if (tid < (PAD ? a.vd : V)) reinterpret_cast<TIn*>(a.out)[b * a.o_s0 + (h0 + n) * a.o_s1 + tid] = from_f32<TIn>(0.0f);
     return;
   }
 
@@ -68,8 +73,9 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
   // without dtype branches, and converted only after the state loads are in
   // flight: a conversion right after its load, or a load inside a branch,
   // would wait for every earlier load (vector loads complete in order).
-  const int kj = tid < K ? tid : 0;
-  const int vj = tid >= kThreads - V ? tid - (kThreads - V) : 0;
+  const int kd = PAD ? a.kd : K, vd = PAD ? a.vd : V;
+  const int kj = tid < kd ? tid : 0;
+  const int vj = tid >= kThreads - V && tid - (kThreads - V) < vd ? tid - (kThreads - V) : 0;
   TIn qr[NH], kr[NH], vr[NH];
   ScalarRaw graw[NH], braw[NH];
 #pragma unroll
@@ -84,22 +90,29 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
 
   float* S[NH];
   f32x4 s[NH][NI];
+  const int ld = PAD ? a.vd : V;  // state row length
+  const bool colin = !PAD || 4 * c4 < a.vd;
 #pragma unroll
   for (int n = 0; n < NH; ++n) {
     S[n] = a.state + slot * a.st_slot + (h0 + n) * a.st_head;
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-      s[n][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S[n] + (int64_t)(r0 + RG * i) * V + 4 * c4));
+    for (int i = 0; i < NI; ++i) {
+      const int r = r0 + RG * i;
+      const bool in = colin && (!PAD || r < a.kd);
+      const f32x4 x = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(S[n] + (in ? (int64_t)r * ld + 4 * c4 : 0)));
+      s[n][i] = in ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
   float g[NH], beta[NH];
 #pragma unroll
   for (int n = 0; n < NH; ++n) {
     if (tid < K) {
-      sq[n][tid] = to_f32(qr[n]) * a.scale;
-      sk[n][tid] = to_f32(kr[n]);
+      sq[n][tid] = tid < kd ? to_f32(qr[n]) * a.scale : 0.f;
+      sk[n][tid] = tid < kd ? to_f32(kr[n]) : 0.f;
     }
-    if (tid >= kThreads - V) sv[n][vj] = to_f32(vr[n]);
+    if (tid >= kThreads - V) sv[n][tid - (kThreads - V)] = tid - (kThreads - V) < vd ? to_f32(vr[n]) : 0.f;
     g[n] = scalar_raw_f32(graw[n], a.g_dtype);
     beta[n] = scalar_raw_f32(braw[n], a.b_dtype);
   }
@@ -179,8 +192,10 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
     for (int j = 0; j < 4; ++j) d[j] = bn * (sv[n][4 * c + j] - eg * kS[j]);
     sd[n][c] = d;
     TIn* o = reinterpret_cast<TIn*>(a.out) + b * a.o_s0 + (h0 + n) * a.o_s1;
+    if (4 * c < vd) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[4 * c + j] = from_f32<TIn>(fmaf(eg, qS[j], qkn * d[j]));
+      for (int j = 0; j < 4; ++j) o[4 * c + j] = from_f32<TIn>(fmaf(eg, qS[j], qkn * d[j]));
+    }
   }
   __syncthreads();
 
@@ -190,25 +205,29 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_step_kernel(RecurrentA
     const f32x4 d = sd[n][c4];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const float kv = sk[n][r0 + RG * i];
+      const int r = r0 + RG * i;
+      const float kv = sk[n][r];
       f32x4 t;
 #pragma unroll
       for (int j = 0; j < 4; ++j) t[j] = fmaf(eg, s[n][i][j], kv * d[j]);
-      __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(S[n] + (int64_t)(r0 + RG * i) * V + 4 * c4));
+      if (colin && (!PAD || r < a.kd)) __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(S[n] + (int64_t)r * ld + 4 * c4));
     }
   }
 }
 
-template <typename TIn, int K, int V>
+template <typename TIn, int K, int V, bool PAD = false>
 hipError_t launch_heads(const RecurrentArgs& a, int64_t nitems, hipStream_t st) {
-  gdn_recurrent_step_kernel<TIn, K, V, 1><<<dim3((unsigned)nitems), dim3(kThreads), 0, st>>>(a);
+  gdn_recurrent_step_kernel<TIn, K, V, 1, PAD><<<dim3((unsigned)nitems), dim3(kThreads), 0, st>>>(a);
   return hipGetLastError();
 }
 
+// 128 x 128 and 64 x 64 have their own instantiations; any other head dims
+// (multiples of 8 up to 128) run zero-padded in the 128 x 128 one.
 template <typename TIn>
 hipError_t launch_dims(const RecurrentArgs& a, int K, int V, int64_t nitems, hipStream_t st) {
   if (K == 128 && V == 128) return launch_heads<TIn, 128, 128>(a, nitems, st);
-  return launch_heads<TIn, 64, 64>(a, nitems, st);
+  if (K == 64 && V == 64) return launch_heads<TIn, 64, 64>(a, nitems, st);
+  return launch_heads<TIn, 128, 128, true>(a, nitems, st);
 }
 
 }  // namespace
@@ -232,6 +251,8 @@ hipError_t gdn_recurrent_step_launch(const gdn_tensor* q, const gdn_tensor* k, c
   a.r = (int32_t)(v->shape[1] / q->shape[1]);
   a.scale = scale;
   a.idx64 = idx->dtype == GDN_DTYPE_I64;
+  a.kd = (int32_t)q->shape[2];
+  a.vd = (int32_t)v->shape[2];
   a.g_dtype = g->dtype;
   a.b_dtype = beta->dtype;
   const int K = (int)q->shape[2], V = (int)v->shape[2];

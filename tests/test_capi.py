@@ -86,7 +86,8 @@ def _call_prefill(a, cu, chunk=64):
         (lambda a: a.update(idx=torch.zeros(2, dtype=torch.float32)), "DTYPE"),
         (lambda a: a.update(q=torch.zeros(2, 2, 256, dtype=torch.bfloat16)[:, :, ::2]), "STRIDE"),
         (lambda a: a.update(state=torch.zeros(3, 4, 128, 256)[..., :128]), "STRIDE"),
-        (lambda a: a.update(**_recurrent_args(K=96, V=96)), "HEAD_DIM"),
+        (lambda a: a.update(**_recurrent_args(K=100, V=96)), "HEAD_DIM"),
+        (lambda a: a.update(**_recurrent_args(K=136, V=128)), "HEAD_DIM"),
     ],
 )
 def test_recurrent_step_validation(mutate, code):

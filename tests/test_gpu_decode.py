@@ -34,6 +34,23 @@ def test_decode_small(dev, K):
     assert torch.equal(st[untouched], case.state[untouched])
 
 
+@pytest.mark.parametrize("K, V", [(32, 32), (128, 64), (64, 128), (96, 40), (8, 8)])
+def test_decode_other_head_dims(dev, K, V):
+    """Head dims other than 64 x 64 and 128 x 128 (multiples of 8 up to 128)
+    run zero-padded in the 128 x 128 kernel; a padding slot among them."""
+    case = decode_case(B=7, num_slots=12, seed=K + V, Hk=2, Hv=4, K=K, V=V)
+    idx = case.idx.clone()
+    idx[3] = -1
+    print(f"decode head dims K={K} V={V}", flush=True)
+    o, st, o_ref, st_ref = _run(case, dev, idx=idx)
+    assert torch.count_nonzero(o[3]) == 0
+    assert_out_close(o, o_ref)
+    assert_state_close(st, st_ref)
+    untouched = torch.ones(12, dtype=torch.bool)
+    untouched[[int(i) for i in idx.tolist() if i >= 0]] = False
+    assert torch.equal(st[untouched], case.state[untouched])
+
+
 def test_decode_fp32_inputs_bf16_beta(dev):
     case = decode_case(B=5, num_slots=9, seed=2, dtype=torch.float32, beta_dtype=torch.bfloat16)
     o, st, o_ref, st_ref = _run(case, dev)
