@@ -94,7 +94,7 @@ struct PrefillArgs {
 //    values, and only then is chunk c + 1's written.
 struct ChunkTiles {
   f16_t k[C * LDK];
-  f16_t q[C * LDK];  // chunk queries; after the Q S products, the output staging (bf16)
+  f16_t q[C * LDK];  // chunk queries (the output is staged in the V tile)
   f16_t p[C * LDH];  // P (fp16), lower triangle
   alignas(16) float gam[C];
   alignas(16) float eg[C];    // e^gamma
