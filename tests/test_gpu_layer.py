@@ -147,3 +147,53 @@ def test_layer_full_shape_4x2048_prefill_128_decode(dev):
     assert_state_close(rec_gpu[used], rec_ref[used], rtol=3e-2, atol=1e-3)
     assert torch.allclose(conv_gpu, conv_ref.float(), rtol=1e-2, atol=1e-2)
 
+
+
+def test_layer_overlapped_decode_matches_serial_order(dev):
+    """In a mixed batch the layer runs its decode step on a second stream,
+    beside the chunked prefill.  The two touch disjoint cache slots, so the
+    output and both caches must equal, bit for bit, the same ops issued in
+    order on one stream (three calls in a row, caches carried)."""
+    from myvllm_amd import chunk_gated_delta_rule, gated_delta_net_decode_step
+    from myvllm_amd.norm import rms_norm_gated
+
+    hidden, Hk, Hv, n_pre, len_pre, n_dec = 512, 4, 8, 4, 600, 64
+    Tp, T = n_pre * len_pre, n_pre * len_pre + n_dec
+    layer = GatedDeltaNet(hidden, Hk, Hv, K, V, device=dev)
+    layer.init_random(std=0.02, seed=7)
+    nslots = n_pre + n_dec
+    cache = LinearAttentionCache(1, nslots, 4, K, V, Hk, Hv, torch.bfloat16, dev, conv_dtype=torch.float32)
+    gen = torch.Generator().manual_seed(8)
+    cache.conv_cache[0].copy_(torch.randn(cache.conv_cache[0].shape, generator=gen))
+    cache.recurrent_cache[0].copy_(torch.randn(cache.recurrent_cache[0].shape, generator=gen) * 0.1)
+    conv_s, rec_s = cache.conv_cache[0].clone(), cache.recurrent_cache[0].clone()
+    idx = torch.randperm(nslots, generator=gen).to(torch.int32).to(dev)
+    cu = cu_from_lengths([len_pre] * n_pre).to(dev)
+    L = layer
+    cz = L.conv_dim + L.v_size
+
+    def serial(x):
+        proj = x @ L.in_proj.t()
+        qkv, z = proj[:, :L.conv_dim], proj[:, L.conv_dim:cz]
+        b, a = proj[:, cz:cz + Hv], proj[:, cz + Hv:]
+        o = torch.empty(T, Hv, V, dtype=x.dtype, device=dev)
+        y = causal_conv1d_fn(qkv[:Tp], L.conv1d_weight, conv_s, idx[:n_pre], cu, l2norm_channels=2 * L.k_size)
+        g, beta = gdn_gating(a[:Tp], b[:Tp], L.A_log, L.dt_bias)
+        chunk_gated_delta_rule(y[:, :L.k_size].view(Tp, Hk, K), y[:, L.k_size:2 * L.k_size].view(Tp, Hk, K),
+                               y[:, 2 * L.k_size:].view(Tp, Hv, V), g, beta, rec_s, idx[:n_pre], cu, out=o[:Tp])
+        gated_delta_net_decode_step(qkv[Tp:], L.conv1d_weight, conv_s, idx[n_pre:], a[Tp:], b[Tp:], L.A_log,
+                                    L.dt_bias, rec_s, idx[n_pre:], Hk, out=o[Tp:])
+        on = rms_norm_gated(o, z.view(T, Hv, V), L.norm_weight, L.rms_norm_eps)
+        return on.view(T, L.v_size) @ L.out_proj.t()
+
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    with torch.no_grad():
+        for call in range(3):
+            x = torch.randn(T, hidden, generator=gen).bfloat16().to(dev)
+            out = layer(x, cu, idx, idx, num_decode_tokens=n_dec)
+            ref = serial(x)
+            torch.cuda.synchronize()
+            print(f"overlapped layer call {call}", flush=True)
+            assert torch.equal(out, ref)
+            assert torch.equal(cache.recurrent_cache[0], rec_s)
+            assert torch.equal(cache.conv_cache[0], conv_s)
