@@ -19,7 +19,11 @@ a 1 GiB copy by a plain HIP streaming kernel) and gives each roofline as a
 fraction of the matching one too.
 
 A step is one call of the op on inputs already resident in HBM.  Timing:
-W untimed warm-up steps, then K steps bracketed by device synchronisation;
+the workload's step runs untimed for ``--settle-ms`` of wall time (default
+300 ms; on an idle GPU the first ~50 launches of a sustained load run in the
+power controller's start-up transient, e.g. the prefill at ~515 us against
+~430 us settled), then W untimed warm-up steps, then K steps bracketed by
+device synchronisation;
 per-launch kernel time from HIP events recorded on the stream the kernel is
 launched on, reported as the median over the K launches (``kernel_ms``, the
 figure the rooflines use) with the mean beside it (``kernel_ms_mean``).  The
@@ -138,6 +142,23 @@ def _cpu_baseline(value, unit, sample) -> dict:
             "cpu_model": info["model"]}
 
 
+class Timing:
+    """ms per step over the timed region, and the per-launch kernel time from
+    the per-step events: median (the reported figure) and mean."""
+
+    def __init__(self, step_ms: float, per: list, back_to_back_ms: float | None = None):
+        self.step_ms = step_ms
+        srt = sorted(per)
+        n = len(srt)
+        self.median_ms = srt[n // 2] if n % 2 else 0.5 * (srt[n // 2 - 1] + srt[n // 2])
+        self.mean_ms = sum(per) / n
+        self.back_to_back_ms = back_to_back_ms
+
+    def fields(self) -> dict:
+        return {"ms_per_step": self.step_ms, "kernel_ms": self.median_ms, "kernel_ms_mean": self.mean_ms}
+
+
+SETTLE_MS = 300.0  # untimed run of each workload before its warm-up (--settle-ms)
 _SLEEP_CYCLES_PER_MS = None
 
 
@@ -158,59 +179,78 @@ def _sleep_cycles_per_ms() -> float:
     return _SLEEP_CYCLES_PER_MS
 
 
-class Timing:
-    """ms per step over the timed region, and the per-launch kernel time from
-    the per-step events: median (the reported figure) and mean."""
-
-    def __init__(self, step_ms: float, per: list, back_to_back_ms: float | None = None):
-        self.step_ms = step_ms
-        srt = sorted(per)
-        n = len(srt)
-        self.median_ms = srt[n // 2] if n % 2 else 0.5 * (srt[n // 2 - 1] + srt[n // 2])
-        self.mean_ms = sum(per) / n
-        self.back_to_back_ms = back_to_back_ms
-
-    def fields(self) -> dict:
-        return {"ms_per_step": self.step_ms, "kernel_ms": self.median_ms, "kernel_ms_mean": self.mean_ms}
+def _settle(fn, ms: float) -> None:
+    """Run fn untimed for `ms` of wall time, so the timed launches see the
+    clock the power controller settles on under this load rather than its
+    start-up transient."""
+    if ms <= 0:
+        return
+    t_end, i = time.perf_counter() + ms * 1e-3, 0
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
 
 
 def _time_gpu(fn, steps: int, warmup: int, back_to_back: bool = False) -> Timing:
     """Run fn() warmup + steps times; return the Timing of the timed steps
-    (per-step HIP events on the launch stream).  The stream is held by a short sleep kernel
-    while the timed steps are enqueued, so they run back to back: a launch that
-    takes less time than the host needs to enqueue it would otherwise be timed
-    together with the host's gaps (the sleep ends before the first timed event).
-    With back_to_back, a second pass of `steps` launches runs with no events
-    between them (one pair around the pass): for a launch of a few
+    (per-step HIP events on the launch stream).  The settle run (SETTLE_MS of
+    wall time) comes first.  Before the timed steps, untimed launches of the
+    same step keep the stream busy while the host enqueues the timed ones, so
+    those run back to back (a launch shorter than the host's enqueue time would
+    otherwise be timed with the host's gaps) and the GPU stays under the same
+    load throughout (an idle stretch, such as a sleep kernel, lets the power
+    controller boost the clock again and the timed launches then start in its
+    transient).  With back_to_back, a second pass of `steps` launches runs with
+    no events between them (one pair around the pass): for a launch of a few
     microseconds the per-step events add several microseconds each, while the
     pass's mean is the launch's time plus only the queue's gap between kernels."""
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
+    _settle(fn, SETTLE_MS)
     stream = torch.cuda.current_stream()
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_probe = max(warmup, 1)
+    w0.record(stream)
+    for i in range(n_probe):
+        fn(i)
+    w1.record(stream)
+    torch.cuda.synchronize()
+    per_ms = max(w0.elapsed_time(w1) / n_probe, 1e-3)
+    # the host enqueues a step (its events included) in well under 60 us; a
+    # step shorter than that cannot keep ahead of the host, so its timed steps
+    # wait behind a sleep kernel of about the enqueue time instead
+    host_ms = 0.06
+    short = per_ms < host_ms and hasattr(torch.cuda, "_sleep")
+    pre = 2 if short else min(256, int(steps * host_ms / per_ms) + 2)
+    sleep_cycles = int((0.2 + steps * host_ms) * _sleep_cycles_per_ms()) if short else 0
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    preroll = hasattr(torch.cuda, "_sleep")  # a private torch helper: without it, no pre-roll
-    cycles = int(min(200.0, 5.0 + 0.2 * steps) * _sleep_cycles_per_ms()) if preroll else 0
-    torch.cuda.synchronize()
-    if preroll:
-        torch.cuda._sleep(cycles)  # longer than the host needs to enqueue the steps
+    base = n_probe
+    for j in range(pre):
+        fn(base + j)
+    base += pre
+    if short:
+        torch.cuda._sleep(sleep_cycles)
     t0.record(stream)
     for i in range(steps):
         evs[i][0].record(stream)
-        fn(warmup + i)
+        fn(base + i)
         evs[i][1].record(stream)
     t1.record(stream)
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
+    base += steps
     b2b = None
     if back_to_back:
-        if preroll:
-            torch.cuda._sleep(cycles)
+        for j in range(pre):
+            fn(base + j)
+        base += pre
+        if short:
+            torch.cuda._sleep(sleep_cycles)
         t0.record(stream)
         for i in range(steps):
-            fn(warmup + steps + i)
+            fn(base + i)
         t1.record(stream)
         torch.cuda.synchronize()
         b2b = t0.elapsed_time(t1) / steps
@@ -737,11 +777,15 @@ def main():
                     help="all, or a comma-separated list of prefill, prefill_short, decode, conv, conv_update, "
                          "decode_fused, "
                          "layer, attn_prefill, attn_paged_prefill, attn_decode, hbm_copy")
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed run of each workload before its warm-up steps, in ms of wall time (0 disables it)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of each CPU-oracle baseline (0 disables it)")
     ap.add_argument("--copy-blocks", type=int, default=None,
                     help="hbm_copy workload: one grid size (workgroups; 0 = one pass) instead of the sweep")
     args = ap.parse_args()
+    global SETTLE_MS
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN path is benchmarked on a single MI355X "
               "(the kernels shard over heads and sequences with no communication inside the ops, so each "
@@ -870,7 +914,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded torch.Generator, CPU-drawn, copied to HBM before timing)",
-        "config": {"workload": workload, "kernel_ms": head["kernel_ms"]},
+        "config": {"workload": workload, "kernel_ms": head["kernel_ms"], "settle_ms": args.settle_ms},
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
     }
