@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_026_903_648,
-    "gdn_chunk_prefill_kernel/short": 3_958_926_576,
-    "gdn_recurrent_step_kernel": 1_083_241_232,
-    "causal_conv1d_varlen_kernel": 665_995_424,
-    "causal_conv1d_step_kernel": 59_315_584,
-    "gdn_decode_fused_kernel": 1_131_518_400,
-    "attn_prefill_kernel": 1_333_713_040,
-    "attn_decode_kernel": 1_269_003_672,  # with its combine kernel
-    "attn_paged_prefill_kernel": 1_186_166_272,
+    "gdn_chunk_prefill_kernel": 1_026_808_064,
+    "gdn_chunk_prefill_kernel/short": 3_938_259_920,
+    "gdn_recurrent_step_kernel": 1_083_260_416,
+    "causal_conv1d_varlen_kernel": 665_989_632,
+    "causal_conv1d_step_kernel": 59_314_368,
+    "gdn_decode_fused_kernel": 1_131_438_608,
+    "attn_prefill_kernel": 1_333_742_240,
+    "attn_decode_kernel": 1_269_022_152,  # with its combine kernel
+    "attn_paged_prefill_kernel": 1_186_454_952,
 }
 
 
