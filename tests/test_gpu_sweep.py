@@ -4,7 +4,8 @@ The other GPU tests pin chosen cases.  This one draws configurations from a
 fixed seed (sequence counts and ragged lengths including empty and one-token
 sequences, head counts and GQA ratios, head dims, input dtypes, decay
 strength, padding slots, int32/int64 index tensors, the prefill's item
-stream) so that combinations no hand-written case names meet the same bars:
+stream, the fused decode step's two caches, the paged decode's key splits)
+so that combinations no hand-written case names meet the same bars:
 bf16/fp16 outputs within rtol 2e-2 / atol 1e-2 (fp32 decode outputs within
 1e-4 / 1e-5), fp32 states within 1e-3 |ref| + 1e-6, conv states bit-exact,
 and every slot outside the batch unchanged bit for bit.
@@ -158,3 +159,58 @@ def test_sweep_paged_prefill(dev, i):
     ref = paged_attention_ref(case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens, case.cu,
                               case.scale)
     assert_attn_close(out, ref)
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_sweep_fused_decode(dev, i):
+    from test_gpu_decode_fused import _check as fused_check
+    from test_gpu_decode_fused import _run as fused_run
+    from myvllm_amd.workloads import decode_fused_case
+
+    r = random.Random(7000 + i)
+    Hk = r.choice([1, 2, 4])
+    dt = r.choice(DTYPES + [torch.float32])
+    c = dict(B=r.randint(1, 24), Hk=Hk, Hv=Hk * r.choice([1, 2, 4]), dtype=dt,
+             cs_dtype=r.choice([torch.float32, dt]), w_dtype=r.choice([torch.float32, dt]),
+             conv_pad=r.random() < 0.3, state_pad=r.random() < 0.3, i64=r.random() < 0.3, steps=r.choice([1, 2]))
+    print(f"sweep fused decode {i}: {c}", flush=True)
+    slots = c["B"] + 3
+    case = decode_fused_case(B=c["B"], num_slots=slots, seed=i, Hk=c["Hk"], Hv=c["Hv"], dtype=c["dtype"],
+                             conv_state_dtype=c["cs_dtype"], weight_dtype=c["w_dtype"])
+    cidx, idx = case.conv_idx.clone(), case.idx.clone()
+    if c["conv_pad"]:
+        cidx[0] = -1
+    if c["state_pad"]:
+        idx[c["B"] - 1] = slots + 5
+    if c["i64"]:
+        cidx, idx = cidx.long(), idx.long()
+    outs, refs, cs, cs_ref, st, st_ref = fused_run(case, dev, cidx=cidx, idx=idx, steps=c["steps"])
+    fused_check(outs, refs, cs, cs_ref, st, st_ref)
+    if c["state_pad"]:
+        assert all(torch.count_nonzero(o[c["B"] - 1]) == 0 for o in outs)
+    used = {int(s) for s in idx.tolist() if 0 <= s < slots}
+    untouched = [s for s in range(slots) if s not in used]
+    assert torch.equal(st[untouched], case.state[untouched])
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_sweep_paged_decode(dev, i):
+    from test_gpu_attention import _decode, _decode_ref
+    from myvllm_amd.workloads import paged_case
+
+    r = random.Random(8000 + i)
+    Hkv = r.choice([1, 2])
+    B = r.randint(1, 12)
+    c = dict(ctx=[r.choice([0, 1, r.randint(2, 600)]) for _ in range(B)], page=r.choice([16, 32, 7]), Hkv=Hkv,
+             Hq=Hkv * r.choice([1, 4, 8, 16]), D=r.choice([64, 128, 256]), dtype=r.choice(DTYPES),
+             splits=r.choice([1, 2, 4, 7]))
+    print(f"sweep paged decode {i}: {c}", flush=True)
+    # one query row per sequence, also for an empty context (its output must be zero)
+    case = paged_case(c["ctx"], [1] * B, page=c["page"], seed=i, Hq=c["Hq"], Hkv=c["Hkv"], D=c["D"],
+                      dtype=c["dtype"])
+    out = _decode(case, dev, c["splits"])
+    ref = _decode_ref(case)
+    assert_attn_close(out, ref)
+    for b, L in enumerate(c["ctx"]):
+        if L == 0:
+            assert torch.count_nonzero(out[b]) == 0
