@@ -784,6 +784,8 @@ def main():
     ap.add_argument("--copy-blocks", type=int, default=None,
                     help="hbm_copy workload: one grid size (workgroups; 0 = one pass) instead of the sweep")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0 or args.settle_ms < 0:
+        ap.error("--steps must be at least 1, --warmup and --settle-ms at least 0")
     global SETTLE_MS
     SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -1,5 +1,6 @@
 """bench.py's command line on the CPU: it measures one GPU only and refuses
-more, and it rejects unknown workloads, before touching a device."""
+more, and it rejects unknown workloads and invalid step counts, before
+touching a device."""
 import os
 import subprocess
 import sys
@@ -23,3 +24,9 @@ def test_world_size_above_one_exits_too():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py")], capture_output=True, text=True, timeout=120,
                        env=env)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_invalid_step_counts_are_refused():
+    for args in (("--steps", "0"), ("--warmup", "-1"), ("--settle-ms", "-5")):
+        r = _run(*args)
+        assert r.returncode == 2 and "--steps must be at least 1" in r.stderr, args
