@@ -28,7 +28,7 @@ def _lastdim_contiguous(t: torch.Tensor) -> torch.Tensor:
 
 
 def chunk_gated_delta_rule(
-    q: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) bf16 or fp16
+    q: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) bf16, fp16 or fp32
     k: torch.Tensor,  # (total_tokens, num_k_heads, k_head_dim) q's dtype
     v: torch.Tensor,  # (total_tokens, num_v_heads, v_head_dim) q's dtype
     g: torch.Tensor,  # (total_tokens, num_v_heads) fp32 log-decay
@@ -47,6 +47,11 @@ def chunk_gated_delta_rule(
         g = g.float()
     if scale is None:
         scale = k.shape[-1] ** -0.5
+    if torch.float32 in (q.dtype, k.dtype, v.dtype):
+        if not q.dtype == k.dtype == v.dtype:
+            raise ValueError(f"q, k and v must share one dtype (got {q.dtype}, {k.dtype}, {v.dtype})")
+        return _chunk_gated_delta_rule_fp32(q, k, v, g, beta, recurrent_state, recurrent_state_indices, cu_seqlens,
+                                            scale, out)
     o = torch.empty(v.shape, dtype=v.dtype, device=dev) if out is None else out
     lib = _lib.load()
     D = _lib.describe
@@ -56,6 +61,38 @@ def chunk_gated_delta_rule(
     )
     _lib.check("gdn_chunk_prefill", rc)
     return o
+
+
+def _chunk_gated_delta_rule_fp32(q, k, v, g, beta, state, idx, cu_seqlens, scale, out):
+    """fp32 q, k, v through the fp16 kernel.  q and k are rounded to fp16, the
+    MFMA operand type (the reference's kernels run their fp32 dots in tf32,
+    whose 10-bit mantissa fp16 matches); v is split exactly enough into
+    v_hi = fp16(v) and v_lo = fp16(v - v_hi) (22 significant bits), and since
+    the recurrence is linear in (state, v) jointly, the kernel runs twice:
+    from the slot's state with v_hi (updating the slot in place) and from a
+    zero state with v_lo (into a temporary); the temporary's final states are
+    added into the slots and o = o_hi + o_lo in fp32.  Two launches; no host
+    synchronisation.  Tokens not covered by any sequence get o = 0."""
+    dev = v.device
+    qh, kh = q.to(torch.float16), k.to(torch.float16)
+    v_hi = v.to(torch.float16)
+    v_lo = (v - v_hi.float()).to(torch.float16)
+    o_hi = torch.zeros(v.shape, dtype=torch.float16, device=dev)
+    o_lo = torch.zeros(v.shape, dtype=torch.float16, device=dev)
+    chunk_gated_delta_rule(qh, kh, v_hi, g, beta, state, idx, cu_seqlens, scale=scale, out=o_hi)
+    n = cu_seqlens.numel() - 1
+    valid = (idx >= 0) & (idx < state.shape[0])
+    tmp_idx = torch.where(valid, torch.arange(n, dtype=torch.int32, device=dev),
+                          torch.full((n,), -1, dtype=torch.int32, device=dev))
+    tmp = torch.zeros((n,) + tuple(state.shape[1:]), dtype=torch.float32, device=dev)
+    chunk_gated_delta_rule(qh, kh, v_lo, g, beta, tmp, tmp_idx, cu_seqlens, scale=scale, out=o_lo)
+    # (a padding sequence adds its zero temporary to slot 0)
+    state.index_add_(0, torch.where(valid, idx.long(), torch.zeros_like(idx, dtype=torch.long)), tmp)
+    o = torch.add(o_hi.float(), o_lo.float())
+    if out is None:
+        return o
+    out.copy_(o)
+    return out
 
 
 def recurrent_gated_delta_rule(

@@ -197,3 +197,29 @@ def test_layer_overlapped_decode_matches_serial_order(dev):
             assert torch.equal(out, ref)
             assert torch.equal(cache.recurrent_cache[0], rec_s)
             assert torch.equal(cache.conv_cache[0], conv_s)
+
+
+def test_layer_fp32_mixed_batch(dev):
+    """The layer in float32 (weights, activations and caches): every op takes
+    fp32, the chunked prefill through its fp32 route (q and k rounded to fp16,
+    v as fp16 hi + lo).  Against the fp64 layer oracle: the output within
+    rtol 1e-2 / atol 1e-3 and the SSM states within 1e-3 relative in norm."""
+    torch.manual_seed(0)
+    layer = GatedDeltaNet(HID, HK, HV, K, V, dtype=torch.float32, device=dev)
+    layer.init_random(seed=11)
+    cache = LinearAttentionCache(1, 6, 4, K, V, HK, HV, torch.float32, dev, conv_dtype=torch.float32)
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    ref_conv, ref_rec = cache.conv_cache[0].cpu().clone(), cache.recurrent_cache[0].cpu().clone()
+    slots = [cache.allocate() for _ in range(5)]
+    g = torch.Generator().manual_seed(12)
+    print("layer fp32 mixed batch", flush=True)
+    for lengths, sl, n_dec, T in (([100, 37], slots[:4], 2, 139), ([70], [slots[4], slots[0], slots[1], slots[2]], 3, 73)):
+        x = torch.randn(T, HID, generator=g)
+        out, ref = _step(layer, cache, x, lengths, sl, n_dec, ref_conv, ref_rec, dev)
+        assert out.dtype == torch.float32
+        assert_out_close(out, ref, rtol=1e-2, atol=1e-3)
+    rec = cache.recurrent_cache[0].cpu().double()
+    used = torch.tensor(slots, dtype=torch.long)
+    rel = ((rec[used] - ref_rec[used].double()).norm() / ref_rec[used].double().norm()).item()
+    assert rel < 1e-3, rel
+    assert torch.allclose(cache.conv_cache[0].cpu().double(), ref_conv.double(), rtol=1e-4, atol=1e-5)

@@ -320,3 +320,36 @@ def test_prefill_wait_give_up_poisons_the_item(dev, monkeypatch):
     monkeypatch.delenv("GDN_PREFILL_SPIN_LIMIT")
     o, st, o_ref, st_ref = _run(case, dev)
     _check(case, o, st, o_ref, st_ref)
+
+
+@pytest.mark.parametrize("lengths,g_scale", [([70, 5, 130, 1], 1.0), ([300, 1000], 0.02)])
+def test_prefill_fp32_inputs(dev, lengths, g_scale):
+    """fp32 q, k, v: q and k are rounded to fp16 (the MFMA operand type, the
+    precision of the tf32 dots the reference's kernels run fp32 in) and v is
+    carried as fp16 hi + lo through two launches.  Bars: the output against
+    the oracle on the raw fp32 inputs within 1e-3 + 2e-3 |ref| (measured
+    <= 0.07 of it); the state against the oracle fed the same fp16-rounded
+    q and k within the usual 1e-3 |ref| + 1e-6 (measured <= 0.17 of it), and
+    against the raw fp32 oracle within 1e-3 relative in norm (measured
+    2.2e-4: the rounding of q and k).  A padding sequence and an untouched
+    slot ride along."""
+    N = len(lengths)
+    case = prefill_case(lengths, seed=3, num_slots=N + 2, Hk=2, Hv=4, dtype=torch.float32, g_scale=g_scale)
+    idx = case.idx.clone()
+    idx[-1] = -1
+    print(f"prefill fp32 inputs {lengths}", flush=True)
+    o, st, o_raw, st_raw = _run(case, dev, idx=idx)
+    assert o.dtype == torch.float32
+    assert_out_close(o, o_raw, rtol=2e-3, atol=1e-3)
+    s, e = int(case.cu[-2]), int(case.cu[-1])
+    assert torch.count_nonzero(o[s:e]) == 0
+    used = torch.tensor([int(i) for i in idx.tolist() if i >= 0], dtype=torch.long)
+    st_r = case.state.clone()
+    chunk_gated_delta_rule_ref(case.q.half().float(), case.k.half().float(), case.v, case.g, case.beta, st_r, idx,
+                               case.cu)
+    assert_state_close(st[used], st_r[used])
+    rel = ((st[used].double() - st_raw[used]).norm() / st_raw[used].norm()).item()
+    assert rel < 1e-3, rel
+    untouched = torch.ones(N + 2, dtype=torch.bool)
+    untouched[used] = False
+    assert torch.equal(st[untouched], case.state[untouched])
