@@ -214,3 +214,31 @@ def test_sweep_paged_decode(dev, i):
     for b, L in enumerate(c["ctx"]):
         if L == 0:
             assert torch.count_nonzero(out[b]) == 0
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_sweep_prefill_fp32(dev, i):
+    """fp32 q/k/v through the prefill's fp32 route: outputs within
+    1e-3 + 2e-3 |ref| of the oracle on the raw inputs, states within the
+    1e-3 |ref| + 1e-6 bar of the oracle fed the same fp16-rounded q and k."""
+    from oracle.gdn import chunk_gated_delta_rule_ref
+
+    c = _prefill_cfg(500 + i)
+    print(f"sweep prefill fp32 {i}: {c}", flush=True)
+    N = len(c["lengths"])
+    case = prefill_case(c["lengths"], seed=500 + i, num_slots=N + 2, Hk=c["Hk"], Hv=c["Hv"], K=c["K"], V=c["V"],
+                        dtype=torch.float32, g_scale=c["g_scale"])
+    idx, cu = case.idx.clone(), case.cu.clone()
+    if c["pad"]:
+        idx[N // 2] = -1
+    if c["i64"]:
+        idx, cu = idx.long(), cu.long()
+    o, st, o_ref, _ = prefill_run(case, dev, idx=idx, cu=cu)
+    assert_out_close(o, o_ref, rtol=2e-3, atol=1e-3)
+    st_r = case.state.clone()
+    chunk_gated_delta_rule_ref(case.q.half().float(), case.k.half().float(), case.v, case.g, case.beta, st_r, idx, cu)
+    used = torch.tensor([int(s) for s in idx.tolist() if 0 <= int(s) < N + 2], dtype=torch.long)
+    assert_state_close(st[used], st_r[used])
+    untouched = torch.ones(N + 2, dtype=torch.bool)
+    untouched[used] = False
+    assert torch.equal(st[untouched], case.state[untouched])
