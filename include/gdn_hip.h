@@ -73,6 +73,7 @@ extern "C" {
 #define GDN_ERR_CONV_WIDTH (-10) /* conv width outside [2, 6] */
 #define GDN_ERR_RANGE (-11)     /* a size exceeds the kernels' index range */
 #define GDN_ERR_SCRATCH (-12)   /* the call needs more than the library's static scratch holds */
+#define GDN_ERR_ARG (-13)       /* an option argument is out of range */
 
 #define GDN_MAX_NDIM 4
 
@@ -117,8 +118,9 @@ int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tenso
  *   out    : (T, Hv, V)  v's dtype, last stride 1
  * chunk_size must be 64; K and V multiples of 8 from 8 to 128 (the
  * reference's k_head_dim <= 128, ops/gated_delta_rule/h.py:211; head dims
- * below 128 run zero-padded to 128, at the cost of 128).  Tokens not covered
- * by any sequence keep whatever `out` held.
+ * below 128 run zero-padded to 128, at the cost of 128).  Output rows of
+ * tokens no sequence covers ([0, cu[0]) and [cu[N], T)) are set to zero, as
+ * the reference allocates o zero-filled (ops/gated_delta_rule/o.py:147).
  * Range: the MFMA operands are fp16, so every q and k row must have an L2
  * norm of at most 128 (the layer's rows are L2-normalised, norm 1) and |v|
  * entries must stay below 65504 (an fp16 out also overflows past 65504, as
@@ -129,13 +131,42 @@ int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tenso
  * Failure: the kernel's wave roles hand work to each other through bounded
  * waits; a wait that gives up (a pipeline error, never expected) writes NaN
  * to all output rows of that (sequence, v-head) and leaves its state slot
- * untouched.  GDN_PREFILL_SPIN_LIMIT in the environment overrides the bound
- * (tests force the give-up path with 0).
+ * untouched.  The environment plays no part in a call.
  */
 int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                       const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                       const gdn_tensor* state_indices, const gdn_tensor* cu_seqlens,
                       gdn_tensor* out, float scale, int32_t chunk_size, void* stream);
+
+/*
+ * gdn_chunk_prefill with options (no counterpart in the reference).  With
+ * flags = 0, items_per_wg = -1 and spin_limit = -1 it is gdn_chunk_prefill.
+ *   flags: GDN_PREFILL_ZERO_INIT    every sequence starts from a zero state
+ *                                   (its slot is not read);
+ *          GDN_PREFILL_ACCUM_STATE  the final state is added to the slot
+ *                                   instead of replacing it;
+ *          GDN_PREFILL_ACCUM_OUT    o is added to out (fp32 out only); rows of
+ *                                   padding or uncovered tokens are left as they are.
+ *   out may be fp32 when q, k and v are fp16 (v's dtype otherwise).  These
+ *   serve fp32 q/k/v: the recurrence is linear in (state, v), so with
+ *   v = v_hi + v_lo (fp16 each) one call with v_hi and fp32 out and a second
+ *   with v_lo, ZERO_INIT | ACCUM_STATE | ACCUM_OUT give the result for v.
+ *   items_per_wg: -1 lets the launcher choose the schedule; 0 is one
+ *     (sequence, v-head) item per workgroup, longest sequence first; 1..64
+ *     deals the items in runs priced by their tokens to ceil(N Hv /
+ *     items_per_wg) workgroups, each walking its run as one chunk stream.
+ *   spin_limit: bound of the kernel's internal waits in sleep iterations,
+ *     0..2^22 (-1: 2^22); 0 forces the give-up path described above (tests).
+ * GDN_ERR_ARG for unknown flags or an option out of range.
+ */
+#define GDN_PREFILL_ZERO_INIT 1
+#define GDN_PREFILL_ACCUM_STATE 2
+#define GDN_PREFILL_ACCUM_OUT 4
+int gdn_chunk_prefill_ex(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                         const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                         const gdn_tensor* state_indices, const gdn_tensor* cu_seqlens,
+                         gdn_tensor* out, float scale, int32_t chunk_size, int32_t flags,
+                         int32_t items_per_wg, int32_t spin_limit, void* stream);
 
 /*
  * Varlen depthwise causal conv1d + SiLU with conv-state carry-in/out

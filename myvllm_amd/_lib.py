@@ -19,6 +19,11 @@ LIB_PATH = os.environ.get("MYVLLM_AMD_LIB") or os.path.join(os.path.dirname(os.p
 ABI_VERSION = 1
 MAX_NDIM = 4
 
+# flags of gdn_chunk_prefill_ex (include/gdn_hip.h)
+PREFILL_ZERO_INIT = 1
+PREFILL_ACCUM_STATE = 2
+PREFILL_ACCUM_OUT = 4
+
 DTYPE_CODES = {
     torch.float32: 0,
     torch.bfloat16: 1,
@@ -30,6 +35,7 @@ DTYPE_CODES = {
 EXPORTED_SYMBOLS = (
     "gdn_recurrent_step",
     "gdn_chunk_prefill",
+    "gdn_chunk_prefill_ex",
     "causal_conv1d_varlen",
     "causal_conv1d_step",
     "gdn_decode_step_fused",
@@ -94,6 +100,8 @@ def load() -> ctypes.CDLL:
         lib.gdn_recurrent_step.argtypes = [_PT] * 8 + [ctypes.c_float, ctypes.c_void_p]
         lib.gdn_chunk_prefill.restype = ctypes.c_int
         lib.gdn_chunk_prefill.argtypes = [_PT] * 9 + [ctypes.c_float, ctypes.c_int32, ctypes.c_void_p]
+        lib.gdn_chunk_prefill_ex.restype = ctypes.c_int
+        lib.gdn_chunk_prefill_ex.argtypes = [_PT] * 9 + [ctypes.c_float] + [ctypes.c_int32] * 4 + [ctypes.c_void_p]
         lib.causal_conv1d_varlen.restype = ctypes.c_int
         lib.causal_conv1d_varlen.argtypes = [_PT] * 6 + [ctypes.c_void_p]
         lib.causal_conv1d_step.restype = ctypes.c_int

@@ -95,7 +95,7 @@ struct AttnArgs {
   const void* cu;
   const void* ctx;
   PagedTable tab;
-  int64_t T;
+  int64_t T, nseq;
   int32_t Hq, Hkv, gh;  // gh: query heads per workgroup (1, 2 or 4)
   float c;              // softmax scale * log2(e)
   bool cu64, ctx64, causal;
@@ -147,7 +147,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // output rows no sequence covers are zero, as the reference allocates o
+  // zero-filled (ops/full_attention.py:467)
+  zero_uncovered_rows<(int)sizeof(T)>(a.o, a.o_st, a.o_sh, a.Hq, D, a.cu, a.cu64, a.nseq, a.T,
+                                      blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z),
+                                      (int64_t)gridDim.x * gridDim.y * gridDim.z, tid, 256);
   const int64_t n = blockIdx.z;
+  if (n >= a.nseq) return;
   const int R = a.Hq / a.Hkv, gh = a.gh, qsubs = 4 / gh, groups = R / gh;
   const int kvh = blockIdx.y / groups;
   const int head = kvh * R + (blockIdx.y % groups) * gh + (w % gh);
@@ -772,8 +778,9 @@ PagedTable paged_table(const gdn_tensor* tab, const gdn_tensor* kc) {
 template <typename T, int D, int BN, bool PAGED>
 hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hipStream_t st) {
   const int qsubs = 4 / a.gh;
-  const int64_t qblocks = (max_len + 32 * qsubs - 1) / (32 * qsubs);
-  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)nseq);
+  // (at least one workgroup, which zeroes the rows no sequence covers)
+  const int64_t qblocks = max_len > 0 ? (max_len + 32 * qsubs - 1) / (32 * qsubs) : 1;
+  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)(nseq > 0 ? nseq : 1));
   if (!PAGED)
     hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 0>), grid, dim3(256), 0, st, a);
   else if (a.tab.page % 16 == 0)
@@ -818,7 +825,7 @@ hipError_t attn_varlen_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, 
                                       const gdn_tensor* cu, gdn_tensor* out, int64_t max_seqlen, float scale,
                                       int causal, hipStream_t st) {
   const int64_t nseq = cu->shape[0] - 1;
-  if (nseq <= 0 || q->shape[0] == 0 || max_seqlen <= 0) return hipSuccess;
+  if (q->shape[0] == 0) return hipSuccess;
   AttnArgs a{};
   a.q = q->data;
   a.q_st = q->stride[0];
@@ -831,6 +838,7 @@ hipError_t attn_varlen_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, 
   a.cu = cu->data;
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
   a.T = q->shape[0];
+  a.nseq = nseq;
   a.Hq = (int32_t)q->shape[1];
   a.Hkv = (int32_t)k->shape[1];
   a.gh = heads_per_group(a.Hq / a.Hkv);
@@ -843,7 +851,7 @@ hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, 
                                      const gdn_tensor* tab, const gdn_tensor* ctx, const gdn_tensor* cu,
                                      gdn_tensor* out, int64_t max_seqlen, float scale, hipStream_t st) {
   const int64_t nseq = cu->shape[0] - 1;
-  if (nseq <= 0 || q->shape[0] == 0 || max_seqlen <= 0) return hipSuccess;
+  if (q->shape[0] == 0) return hipSuccess;
   AttnArgs a{};
   a.q = q->data;
   a.q_st = q->stride[0];
@@ -859,6 +867,7 @@ hipError_t attn_paged_prefill_launch(const gdn_tensor* q, const gdn_tensor* kc, 
   a.ctx64 = ctx->dtype == GDN_DTYPE_I64;
   a.tab = paged_table(tab, kc);
   a.T = q->shape[0];
+  a.nseq = nseq;
   a.Hq = (int32_t)q->shape[1];
   a.Hkv = (int32_t)kc->shape[2];
   a.gh = heads_per_group(a.Hq / a.Hkv);

@@ -184,6 +184,11 @@ GDN_DEVICE void conv_tile(const ConvArgs& a, int64_t seq, int64_t tile, int64_t 
 template <typename TX, typename TW, typename TS, int W>
 __global__ __launch_bounds__(kThreads) void causal_conv1d_varlen_kernel(ConvArgs a) {
   __shared__ int32_t lds[8];
+  // output rows no sequence covers are zero, as the reference allocates y
+  // zero-filled (ops/causal_conv1d.py:241)
+  zero_uncovered_rows<(int)sizeof(TX)>(a.out, a.o_s0, 0, 1, a.D, a.cu, a.cu64, a.nseq, a.T,
+                                       (int64_t)blockIdx.x * gridDim.y + blockIdx.y, (int64_t)gridDim.x * gridDim.y,
+                                       threadIdx.x, kThreads);
   const int64_t d0 = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * kCh;
   const bool active = d0 < a.D;
   // the taps depend only on the channel block: their loads overlap the lookup

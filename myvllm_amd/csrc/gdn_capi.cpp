@@ -7,7 +7,6 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
-#include <cstdlib>
 #include <stdint.h>
 
 #include "../../include/gdn_hip.h"
@@ -18,7 +17,7 @@ hipError_t gdn_recurrent_step_launch(const gdn_tensor* q, const gdn_tensor* k, c
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    int32_t spin_limit, int32_t items_per_wg, hipStream_t st);
+                                    int32_t flags, int32_t spin_limit, int32_t items_per_wg, hipStream_t st);
 hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
                                        int64_t norm_ch, hipStream_t st);
@@ -102,7 +101,7 @@ bool vec_ok(const gdn_tensor* t, int vec_bytes) {
 
 int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v, const gdn_tensor* g,
                     const gdn_tensor* beta, const gdn_tensor* state, const gdn_tensor* idx,
-                    const gdn_tensor* out, const gdn_tensor* cu, bool prefill) {
+                    const gdn_tensor* out, const gdn_tensor* cu, bool prefill, bool f32_out = false) {
   GDN_TRY(check_desc(q, 3));
   GDN_TRY(check_desc(k, 3));
   GDN_TRY(check_desc(v, 3));
@@ -128,7 +127,9 @@ int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* 
   if (Hk <= 0 || Hv % Hk != 0) return GDN_ERR_HEADS;
 
   // dtypes
-  if (k->dtype != q->dtype || v->dtype != q->dtype || out->dtype != v->dtype) return GDN_ERR_DTYPE;
+  if (k->dtype != q->dtype || v->dtype != q->dtype) return GDN_ERR_DTYPE;
+  if (f32_out ? (q->dtype != GDN_DTYPE_F16 || out->dtype != GDN_DTYPE_F32) : out->dtype != v->dtype)
+    return GDN_ERR_DTYPE;
   if (!is_float(q->dtype) || !is_float(g->dtype) || !is_float(beta->dtype)) return GDN_ERR_DTYPE;
   if (state->dtype != GDN_DTYPE_F32 || !is_index(idx->dtype)) return GDN_ERR_DTYPE;
   if (prefill && ((q->dtype != GDN_DTYPE_BF16 && q->dtype != GDN_DTYPE_F16) || g->dtype != GDN_DTYPE_F32 ||
@@ -256,30 +257,8 @@ int check_fused(const gdn_tensor* x, const gdn_tensor* w, const gdn_tensor* cs, 
 int launch_rc(hipError_t e) { return e == hipSuccess ? GDN_OK : (int)e; }
 
 // Bound of the prefill kernel's internal waits between its wave roles (sleep
-// iterations; never reached when the pipeline is correct).  The environment
-// variable GDN_PREFILL_SPIN_LIMIT overrides it so that a test can force the
-// give-up path (NaN output, state untouched) with every wave still exiting.
-int32_t prefill_spin_limit() {
-  constexpr int32_t kDefault = 1 << 22;
-  const char* env = std::getenv("GDN_PREFILL_SPIN_LIMIT");
-  if (!env || !*env) return kDefault;
-  char* end = nullptr;
-  const long v = std::strtol(env, &end, 10);
-  return (end && *end == 0 && v >= 0 && v <= kDefault) ? (int32_t)v : kDefault;
-}
-
-// Items (sequence, v-head) per prefill workgroup: -1 lets the launcher choose
-// (several consecutive items per workgroup for batches of short sequences,
-// one otherwise).  GDN_PREFILL_ITEMS_PER_WG in the environment fixes it (0: one
-// item per workgroup, longest first; 1..64: that many consecutive items), so
-// that a test can run both schedules on the same inputs.
-int32_t prefill_items_per_wg() {
-  const char* env = std::getenv("GDN_PREFILL_ITEMS_PER_WG");
-  if (!env || !*env) return -1;
-  char* end = nullptr;
-  const long v = std::strtol(env, &end, 10);
-  return (end && *end == 0 && v >= 0 && v <= 64) ? (int32_t)v : -1;
-}
+// iterations; never reached when the pipeline is correct).
+constexpr int32_t kPrefillSpinLimit = 1 << 22;
 
 constexpr int64_t kMaxGridYZ = 65535;
 constexpr int32_t kMaxDecodeSplits = 256;
@@ -337,6 +316,7 @@ GDN_EXPORT const char* gdn_strerror(int code) {
     case GDN_ERR_ALIGN: return "pointer or stride misaligned for 16-byte vector access";
     case GDN_ERR_CONV_WIDTH: return "conv width must be in [2, 6]";
     case GDN_ERR_RANGE: return "size exceeds the kernels' index range";
+    case GDN_ERR_ARG: return "an option argument is out of range";
     case GDN_ERR_SCRATCH: return "the call needs more split scratch than the library's static array holds "
                                  "(GDN_DECODE_SCRATCH_FLOATS fp32 values); use fewer splits or the workspace entry";
     default: break;
@@ -359,8 +339,25 @@ GDN_EXPORT int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const
                                  gdn_tensor* out, float scale, int32_t chunk_size, void* stream) {
   if (chunk_size != 64) return GDN_ERR_CHUNK;
   GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, cu_seqlens, true));
-  return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale,
-                                            prefill_spin_limit(), prefill_items_per_wg(),
+  return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale, 0,
+                                            kPrefillSpinLimit, -1, reinterpret_cast<hipStream_t>(stream)));
+}
+
+GDN_EXPORT int gdn_chunk_prefill_ex(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
+                                    const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
+                                    const gdn_tensor* state_indices, const gdn_tensor* cu_seqlens,
+                                    gdn_tensor* out, float scale, int32_t chunk_size, int32_t flags,
+                                    int32_t items_per_wg, int32_t spin_limit, void* stream) {
+  if (chunk_size != 64) return GDN_ERR_CHUNK;
+  constexpr int32_t kKnown = GDN_PREFILL_ZERO_INIT | GDN_PREFILL_ACCUM_STATE | GDN_PREFILL_ACCUM_OUT;
+  if ((flags & ~kKnown) != 0 || items_per_wg < -1 || items_per_wg > 64 || spin_limit < -1 ||
+      spin_limit > kPrefillSpinLimit)
+    return GDN_ERR_ARG;
+  const bool f32_out = out && out->dtype == GDN_DTYPE_F32;
+  if ((flags & GDN_PREFILL_ACCUM_OUT) && !f32_out) return GDN_ERR_DTYPE;
+  GDN_TRY(check_recurrent(q, k, v, g, beta, state, state_indices, out, cu_seqlens, true, f32_out));
+  return launch_rc(gdn_chunk_prefill_launch(q, k, v, g, beta, state, state_indices, cu_seqlens, out, scale, flags,
+                                            spin_limit < 0 ? kPrefillSpinLimit : spin_limit, items_per_wg,
                                             reinterpret_cast<hipStream_t>(stream)));
 }
 

@@ -181,6 +181,35 @@ GDN_DEVICE void seq_range(const void* cu, bool cu64, int64_t n, int64_t T, int64
   e = b;
 }
 
+// Rows of a packed (T, H, Dv) output that no sequence covers -- [0, cu[0])
+// and [cu[N], T), clamped like seq_range -- are set to zero, as the
+// reference's ops allocate their outputs zero-filled (torch.zeros_like).
+// The work is shared by all workgroups of a launch (a grid-stride loop over
+// 16-byte vectors of those rows); when the sequences cover [0, T), the usual
+// case, each thread only reads cu[0] and cu[N].  Dv * ES must be a multiple of
+// 16 and rows 16-byte aligned (checked on the host).  Not inlined: its
+// 64-bit index arithmetic would otherwise shape the register allocation of
+// the whole kernel that calls it first thing.
+template <int ES>
+__device__ __attribute__((noinline)) void zero_uncovered_rows(void* out, int64_t s0, int64_t s1, int64_t H, int64_t Dv, const void* cu,
+                                    bool cu64, int64_t nseq, int64_t T, int64_t wg, int64_t nwg, int64_t tid,
+                                    int64_t nthreads) {
+  int64_t first = load_index(cu, 0, cu64), last = load_index(cu, nseq, cu64);
+  first = first < 0 ? 0 : (first > T ? T : first);
+  last = last < first ? first : (last > T ? T : last);
+  const int64_t nrows = first + (T - last);
+  if (nrows == 0) return;
+  typedef uint32_t u32x4z __attribute__((ext_vector_type(4)));
+  constexpr int64_t per = 16 / ES;  // elements per 16-byte vector
+  const int64_t vph = Dv / per, vpr = H * vph;
+  for (int64_t i = wg * nthreads + tid; i < nrows * vpr; i += nwg * nthreads) {
+    const int64_t r = i / vpr, rem = i - r * vpr;
+    const int64_t h = rem / vph, c = (rem - h * vph) * per;
+    const int64_t t = r < first ? r : last + (r - first);
+    *reinterpret_cast<u32x4z*>(reinterpret_cast<char*>(out) + (t * s0 + h * s1 + c) * ES) = u32x4z{0u, 0u, 0u, 0u};
+  }
+}
+
 
 // Sum over the 16 lanes of a DPP row, on every lane of the row (quad swaps,
 // then the half-row and row mirrors).

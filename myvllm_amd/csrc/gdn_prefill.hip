@@ -81,8 +81,9 @@ struct PrefillArgs {
   int32_t b_dtype;
   float scale;
   int32_t spin_limit;  // bound of a producer wait (sleep iterations)
-  int32_t per_wg;      // items per workgroup: 0 = one item, longest first; else consecutive work ids
+  int32_t per_wg;      // 0: one item per workgroup, longest first; > 0: runs of work ids dealt by cost
   int32_t kd, vd;      // key and value head dims (multiples of 8 up to 128; smaller ones run zero-padded)
+  int32_t flags;       // GDN_PREFILL_ZERO_INIT | GDN_PREFILL_ACCUM_STATE | GDN_PREFILL_ACCUM_OUT
   bool idx64, cu64;
 };
 
@@ -874,13 +875,14 @@ GDN_DEVICE int out_slot(int s, int m) {
 }
 
 // The state products of one chunk on this wave's 32 value columns; writes the
-// chunk's output rows for those columns (staged through its own columns of
-// the V tile, after which it signals v_free).  The state is held in units of
+// chunk's output rows for those columns (16-bit outputs are staged through its
+// own columns of the V tile, fp32 outputs (OUT32) are stored straight from the
+// accumulators; then it signals v_free).  The state is held in units of
 // 2^su (true state = S * 2^su; su is per value column, since no product
 // mixes value columns): the update rescales S by one factor per chunk and
 // picks the new units from the exponents of V' and of the decayed state, so
 // S stays below 2^14 and is split without another pass over it.
-template <bool F16, bool PAD>
+template <bool F16, bool PAD, bool OUT32>
 GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, bf16_t* vt, int32_t* v_free,
                               f32x16 (&S)[4], int& su, float& sb, const PrefillArgs& a, int64_t c0, int L, int h,
                               int wave, int lane) {
@@ -979,12 +981,35 @@ GDN_DEVICE void consume_chunk(const ChunkTiles& ct, const TBuf& tb, float kn2, b
 #pragma unroll
     for (int mt = (ks >> 1); mt < 2; ++mt) QS[mt] = mfma32(frag_rows(ct.p, LDH, 32 * mt, 16 * ks, lane), vb, QS[mt]);
   }
+  if constexpr (OUT32) {
+    // fp32 output straight from the accumulators: lane (n, g) holds column
+    // 32 wave + n of rows 32 mt + 8 i + 4 g + rr; one store instruction
+    // covers 32 consecutive columns of two rows.  GDN_PREFILL_ACCUM_OUT adds
+    // to what out holds.
+    const float osc = __builtin_amdgcn_ldexpf(a.scale, er);
+    const bool acc = (a.flags & GDN_PREFILL_ACCUM_OUT) != 0;
+    float* ob = reinterpret_cast<float*>(a.out) + c0 * a.o_s0 + h * a.o_s1 + 32 * wave + n;
+    if (!PAD || 32 * wave + n < a.vd) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int row = 32 * mt + 8 * i + 4 * gq + rr;
+            if (row < L) {
+              float* p = ob + (uint32_t)row * (uint32_t)a.o_s0;
+              const float o = QS[mt][4 * i + rr] * osc;
+              *p = acc ? *p + o : o;
+            }
+          }
+    }
+  } else {
   // Stage this wave's output columns (bf16) in its own columns of the V tile,
   // column-major: output column m's rows 32 h .. 32 h + 31 sit in tile row
   // 2 m + h, in eight 4-row slots permuted by out_slot (conflict-free 8-byte
   // writes and transposed reads).  Each lane writes 4 consecutive rows of its
   // column at once, then reads back 16-byte row pieces with transposed reads.
-  {
     const float osc = __builtin_amdgcn_ldexpf(a.scale, er);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -1149,55 +1174,83 @@ GDN_DEVICE void item_fields(const PrefillArgs& a, int64_t seq, int h, Items& it)
   it.nc = (pad || it.e <= it.s) ? 0 : (int32_t)((it.e - it.s + C - 1) / C);
 }
 
-// MULTI: several items per workgroup (a.per_wg > 0); the one-item schedule
-// is its own instantiation, so the long-sequence path pays nothing for the
-// item stream.
+// ---- several items per workgroup: runs of work ids dealt by cost ------------
+//
+// Work ids are sequence-major (w = sequence * Hv + v-head), so the v-heads of
+// a k-head, and all heads of a sequence, are neighbours.  An item is priced
+// at its token count plus kItemCost tokens (what an item boundary costs: the
+// state store and the next state's load take about 0.6 of a 64-token chunk
+// step), and workgroup b of nwg takes the items whose price interval starts
+// in [b P / nwg, (b + 1) P / nwg), P the batch's total price.  Prices are a
+// closed form of cu_seqlens, so every wave finds its run's ends by two
+// searches over cu_seqlens, with no pass over the batch and no host sync; a
+// long sequence among many short ones is thereby spread over workgroups
+// instead of sharing one with all of its v-heads.
+constexpr int64_t kItemCost = 40;
+
+// Price of the items before sequence s, per v-head (cu clamped like seq_range).
+GDN_DEVICE int64_t price_before(const PrefillArgs& a, int64_t s) {
+  int64_t c0 = load_index(a.cu, 0, a.cu64), cs = load_index(a.cu, s, a.cu64);
+  c0 = c0 < 0 ? 0 : (c0 > a.T ? a.T : c0);
+  cs = cs < c0 ? c0 : (cs > a.T ? a.T : cs);
+  return (cs - c0) + kItemCost * s;
+}
+
+// First work id whose price interval starts at or after `target` (all lanes
+// of the wave take part; a 64-ary search over the sequences, one probe per
+// lane per round, so two rounds cover 4096 sequences).
+GDN_DEVICE int64_t first_item_at(const PrefillArgs& a, int64_t target, int lane) {
+  const int64_t Hv = a.Hv;
+  // largest s in [0, nseq] with Hv * price_before(s) <= target (true at s = 0)
+  int64_t lo = 0, span = a.nseq + 1;
+  while (span > 1) {
+    const int64_t step = (span + 63) / 64;
+    const int64_t s = lo + lane * step;
+    const int64_t sl = s < a.nseq ? s : a.nseq;  // (every lane loads inside cu_seqlens)
+    const bool ok = s < lo + span && Hv * price_before(a, sl) <= target;
+    const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));  // >= 1: lane 0 probes lo
+    const int64_t nlo = lo + (int64_t)(cnt - 1) * step;
+    span = (lo + span - nlo) < step ? (lo + span - nlo) : step;
+    lo = nlo;
+  }
+  if (lo >= a.nseq) return a.nseq * Hv;
+  const int64_t p0 = Hv * price_before(a, lo);
+  const int64_t c = price_before(a, lo + 1) - price_before(a, lo);  // >= kItemCost
+  const int64_t h = (target - p0 + c - 1) / c;  // first v-head of sequence lo starting at or after target
+  return h >= Hv ? (lo + 1) * Hv : lo * Hv + h;
+}
+
+// This workgroup's run [w0, w1) of work ids; workgroup b's w1 is workgroup
+// b + 1's w0 (the same expression), so the runs tile [0, nseq Hv).
+GDN_DEVICE void multi_run(const PrefillArgs& a, int64_t bid, int64_t nwg, int lane, int64_t& w0, int64_t& w1) {
+  const int64_t total = a.Hv * price_before(a, a.nseq);
+  const int64_t q = total / nwg, r = total % nwg;
+  auto target = [&](int64_t b) { return q * b + (r * b) / nwg; };  // floor(total b / nwg) without overflow
+  w0 = bid == 0 ? 0 : first_item_at(a, target(bid), lane);
+  w1 = bid + 1 >= nwg ? a.nseq * a.Hv : first_item_at(a, target(bid + 1), lane);
+}
+
+// All roles walk the chunk stream of the items in `it` (every role executes
+// exactly 1 + nq workgroup barriers, nq = chunks in the stream).
 // PAD: head dims below 128, zero-padded to 128 in the tiles and the state
 // registers (zero key columns and zero value columns leave the rest exact).
-template <bool F16, bool MULTI, bool PAD>
-__global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
-  __shared__ Smem sm;
-
-  const int tid = threadIdx.x;
+// OUT32: fp32 output (q, k, v fp16).
+template <bool F16, bool MULTI, bool PAD, bool OUT32>
+GDN_DEVICE void run_items(Smem& sm, const PrefillArgs& a, const Items& it, int tid) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t bid = blockIdx.x;
-  const int64_t nwork = a.nseq * a.Hv;
-
-  // One item per workgroup: consecutive v-heads (sharing a k-head) go to one
-  // XCD (workgroups are dealt round-robin over the 8 XCDs), sequences longest
-  // first.  Several items per workgroup: a contiguous run of work ids, whose
-  // v-head pairs then share the workgroup's L2.
-  const int64_t work = MULTI ? bid * a.per_wg : 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
-  if (work >= nwork) return;
-  if (tid == 0) {
-    sm.kv_ready = 0;
-    sm.v_free = 0;
-    sm.pro = 0;
-    sm.failed = 0;
-  }
-  __syncthreads();  // the counters are zero before any wave can arrive
-  Items it;
-  if (!MULTI) {
-    it.m = 1;
-    item_fields(a, seq_of_rank(sm, a, work / a.Hv, tid), (int)(work % a.Hv), it);
-  } else {
-    const int64_t left = nwork - work;
-    it.m = (int)(left < a.per_wg ? left : a.per_wg);
-    const int64_t w = work + (lane < it.m ? lane : 0);
-    item_fields(a, w / a.Hv, (int)(w % a.Hv), it);
-  }
-  // padding sequences: zero output rows, no state
+  // padding sequences: zero output rows, no state (GDN_PREFILL_ACCUM_OUT: nothing to add)
+  constexpr int kVec = OUT32 ? 4 : 8;  // output elements per 16-byte vector
+  constexpr int kLanesPerRow = VD / kVec;
   for (int j = 0; j < it.m; ++j) {
-    if (rd32(it.slot, j) >= 0) continue;
+    if (rd32(it.slot, j) >= 0 || (a.flags & GDN_PREFILL_ACCUM_OUT)) continue;
     const int64_t s = rd64(it.s, j), e = rd64(it.e, j);
     const int h = rd32(it.h, j);
-    if (PAD && 8 * (tid & 15) >= a.vd) continue;  // (no barrier or cross-lane step follows in this loop)
-    for (int64_t t = s + (tid >> 4); t < e; t += kThreads / 16) {
-      bf16x8 z;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) z[m] = (bf16_t)0.f;
-      *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + h * a.o_s1 + 8 * (tid & 15)) = z;
+    const int col = kVec * (tid % kLanesPerRow);
+    if (PAD && col >= a.vd) continue;  // (no barrier or cross-lane step follows in this loop)
+    for (int64_t t = s + tid / kLanesPerRow; t < e; t += kThreads / kLanesPerRow) {
+      char* p = reinterpret_cast<char*>(a.out) + (t * a.o_s0 + h * a.o_s1 + col) * (OUT32 ? 4 : 2);
+      *reinterpret_cast<u32x4*>(p) = u32x4{0u, 0u, 0u, 0u};
     }
   }
   int nq = 0;  // chunks in the stream
@@ -1218,6 +1271,13 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     // (the state's lane offsets are recomputed at each load and store rather
     // than held in registers across the chunk loop)
     auto load_state = [&](const ChunkAt& ch) __attribute__((always_inline)) {
+      if (a.flags & GDN_PREFILL_ZERO_INIT) {  // start from zero; the slot is not read
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) S[mt] = zero16();
+        su = 0;
+        sb = 0.f;
+        return;
+      }
       int ln = lane;
       asm volatile("" : "+v"(ln));
       if constexpr (PAD) {
@@ -1255,7 +1315,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     __syncthreads();  // chunk 0 is prepared
     for (int q = 0; q < nq; ++q) {
       const ChunkAt ch = chunk_at(it, p);
-      consume_chunk<F16, PAD>(sm.tiles[q & 1], sm.tb[q % 3], fmaxf(sm.kn2[q % 3][0], sm.kn2[q % 3][1]), sm.v, &sm.v_free,
+      consume_chunk<F16, PAD, OUT32>(sm.tiles[q & 1], sm.tb[q % 3], fmaxf(sm.kn2[q % 3][0], sm.kn2[q % 3][1]), sm.v, &sm.v_free,
                          S, su, sb, a, ch.c0, ch.L, ch.h, wave, lane);
       // the carried bound only grows looser: every 16 chunks it is replaced by the exact maximum
       if ((p.c & 15) == 15) sb = col_max(S, 4);
@@ -1267,15 +1327,26 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
         // every later item of the workgroup fails the same way)
         const int64_t s0 = rd64(it.s, p.j);
         if (__hip_atomic_load(&sm.failed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
-          asm volatile("");
-          const s16x4 nan4 =
-              from_f32x4<F16>((f32x4){__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")});
-          const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3],
-                                                              nan4[0], nan4[1], nan4[2], nan4[3]});
-          if (!PAD || 32 * wave + 8 * (lane & 3) < a.vd)
-            for (int64_t t = s0 + (lane >> 2); t < ch.e; t += 16)
-              *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+          // (the NaN is made opaque here so that it is not materialised, and
+          // kept in registers, ahead of the chunk loop)
+          float nan = __builtin_nanf("");
+          asm volatile("" : "+v"(nan));
+          if constexpr (OUT32) {
+            if (!PAD || 32 * wave + 4 * (lane & 7) < a.vd)
+              for (int64_t t = s0 + (lane >> 3); t < ch.e; t += 8)
+                *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave +
+                                          4 * (lane & 7)) = f32x4{nan, nan, nan, nan};
+          } else {
+            const s16x4 nan4 = from_f32x4<F16>((f32x4){nan, nan, nan, nan});
+            const bf16x8 z = __builtin_bit_cast(bf16x8, (s16x8){nan4[0], nan4[1], nan4[2], nan4[3],
+                                                                nan4[0], nan4[1], nan4[2], nan4[3]});
+            if (!PAD || 32 * wave + 8 * (lane & 3) < a.vd)
+              for (int64_t t = s0 + (lane >> 2); t < ch.e; t += 16)
+                *reinterpret_cast<bf16x8*>(a.out + t * a.o_s0 + ch.h * a.o_s1 + 32 * wave + 8 * (lane & 3)) = z;
+          }
         } else {
+          // the final state goes back to the slot (GDN_PREFILL_ACCUM_STATE: is added to it)
+          const bool acc = (a.flags & GDN_PREFILL_ACCUM_STATE) != 0;
           int ln = lane;
           asm volatile("" : "+v"(ln));
           if constexpr (PAD) {
@@ -1286,8 +1357,19 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
 #pragma unroll
               for (int j = 0; j < 16; ++j) {
                 const int r = 32 * mt + 8 * (j >> 2) + (j & 3) + 4 * (ln >> 5);
-                if (r < a.kd && c < a.vd) Sb[r * a.vd + c] = __builtin_amdgcn_ldexpf(S[mt][j], su);
+                if (r < a.kd && c < a.vd) {
+                  const float x = __builtin_amdgcn_ldexpf(S[mt][j], su);
+                  Sb[r * a.vd + c] = acc ? Sb[r * a.vd + c] + x : x;
+                }
               }
+          } else if (acc) {
+            asm volatile("");
+            float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+              for (int j = 0; j < 16; ++j)
+                Sg[(32 * mt + 8 * (j >> 2) + (j & 3)) * VD] += __builtin_amdgcn_ldexpf(S[mt][j], su);
           } else {
             float* Sg = state_of(ch) + (4 * (ln >> 5)) * VD + 32 * wave + (ln & 31);
 #pragma unroll
@@ -1368,7 +1450,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
     if constexpr (MULTI && !PAD)
       if (pp.j < it.m) pp = next_pos(it, pp);
     auto touch = [&]() __attribute__((always_inline)) {
-      if (pp.j < it.m && pp.c == 0) {
+      if (pp.j < it.m && pp.c == 0 && !(a.flags & GDN_PREFILL_ZERO_INIT)) {
         const ChunkAt ch = chunk_at(it, pp);
         const uint32_t* src = reinterpret_cast<const uint32_t*>(a.state + (int64_t)ch.slot * a.st_slot +
                                                                 ch.h * a.st_head) + pw * (KD * VD / 2) + 16 * lane;
@@ -1482,12 +1564,90 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs
   }
 }
 
+GDN_DEVICE void reset_counters(Smem& sm) {
+  sm.kv_ready = 0;
+  sm.v_free = 0;
+  sm.pro = 0;
+  sm.failed = 0;
+}
+
+// MULTI: several items per workgroup (a.per_wg > 0), dealt by cost; the
+// one-item schedule is its own instantiation, so the long-sequence path pays
+// nothing for the item stream.
+template <bool F16, bool MULTI, bool PAD, bool OUT32>
+__global__ __launch_bounds__(kThreads) void gdn_chunk_prefill_kernel(PrefillArgs a) {
+  __shared__ Smem sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int64_t bid = blockIdx.x;
+  const int64_t nwork = a.nseq * a.Hv;
+
+  if (!(a.flags & GDN_PREFILL_ACCUM_OUT))
+    zero_uncovered_rows<OUT32 ? 4 : 2>(a.out, a.o_s0, a.o_s1, a.Hv, a.vd, a.cu, a.cu64, a.nseq, a.T, bid, gridDim.x,
+                                       tid, kThreads);
+  if constexpr (!MULTI) {
+    // One item per workgroup: consecutive v-heads (sharing a k-head) go to one
+    // XCD (workgroups are dealt round-robin over the 8 XCDs), sequences
+    // longest first.
+    const int64_t work = 2 * ((bid >> 4) * 8 + (bid & 7)) + ((bid >> 3) & 1);
+    if (work >= nwork) return;
+    if (tid == 0) reset_counters(sm);
+    __syncthreads();  // the counters are zero before any wave can arrive
+    Items it;
+    it.m = 1;
+    item_fields(a, seq_of_rank(sm, a, work / a.Hv, tid), (int)(work % a.Hv), it);
+    run_items<F16, MULTI, PAD, OUT32>(sm, a, it, tid);
+  } else {
+    // A run of work ids, walked as streams of up to 64 items (one item per
+    // lane of the item table); the v-head pairs of a k-head are consecutive
+    // and share the workgroup's L2.
+    int64_t w0, w1;
+    multi_run(a, bid, gridDim.x, lane, w0, w1);
+    for (int64_t base = w0; base < w1; base += 64) {
+      // (an opaque thread index and an opaque pointer to the kernel
+      // arguments per stream: nothing lane-dependent and no argument load is
+      // hoisted out of this loop, where it would stay live across every
+      // stream; the arguments are the kernel's only ones, at offset 0 of its
+      // argument segment)
+      int t = tid;
+      asm volatile("" : "+v"(t));
+#if defined(__HIP_DEVICE_COMPILE__)
+      typedef const __attribute__((address_space(4))) PrefillArgs* KernArgs;
+      KernArgs kp = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(kp));
+      const PrefillArgs as = *kp;  // (scalar loads from the constant address space)
+#else
+      const PrefillArgs& as = a;  // (the host pass only checks the kernel)
+#endif
+      if (t == 0) reset_counters(sm);
+      __syncthreads();  // the counters are zero before any wave can arrive
+      Items it;
+      it.m = (int)(w1 - base < 64 ? w1 - base : 64);
+      const int64_t w = base + ((t & 63) < it.m ? (t & 63) : 0);
+      item_fields(as, w / as.Hv, (int)(w % as.Hv), it);
+      run_items<F16, MULTI, PAD, OUT32>(sm, as, it, t);
+      __syncthreads();  // every role has left the stream before the counters are reset
+    }
+  }
+}
+
 }  // namespace
+
+// CUs of the device the stream runs on (the schedule heuristic's unit).
+static int64_t stream_cu_count(hipStream_t st) {
+  hipDevice_t dev = 0;
+  int cus = 0;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;  // (an MI355X; the result only shapes the schedule)
+  return cus;
+}
 
 hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                                     const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
                                     const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out, float scale,
-                                    int32_t spin_limit, int32_t items_per_wg, hipStream_t st) {
+                                    int32_t flags, int32_t spin_limit, int32_t items_per_wg, hipStream_t st) {
   PrefillArgs a;
   a.q = reinterpret_cast<const bf16_t*>(q->data);
   a.k = reinterpret_cast<const bf16_t*>(k->data);
@@ -1513,43 +1673,49 @@ hipError_t gdn_chunk_prefill_launch(const gdn_tensor* q, const gdn_tensor* k, co
   a.b_dtype = beta->dtype;
   a.scale = scale;
   a.spin_limit = spin_limit;
+  a.flags = flags;
   a.idx64 = idx->dtype == GDN_DTYPE_I64;
   a.cu64 = cu->dtype == GDN_DTYPE_I64;
   a.kd = (int32_t)q->shape[2];
   a.vd = (int32_t)v->shape[2];
   const int64_t nwork = a.nseq * a.Hv;
-  if (nwork == 0 || a.T == 0) return hipSuccess;
+  if (a.T == 0) return hipSuccess;
   // Batches of short sequences (at most two chunks on average) with at least
-  // two items per CU: each workgroup walks up to 64 consecutive items as one
-  // chunk stream, so that the next item's pipeline fill overlaps the current
-  // item's chunks.  Otherwise one item per workgroup, longest first.
-  constexpr int64_t kCUs = 256;  // MI355X
+  // two items per CU: each workgroup walks a run of about `per` items priced
+  // by their tokens as one chunk stream, so that the next item's pipeline
+  // fill overlaps the current item's chunks.  Otherwise one item per
+  // workgroup, longest first.
   if (items_per_wg < 0) {
-    const bool short_items = a.T <= 2 * C * a.nseq && nwork >= 2 * kCUs;
-    const int64_t per = (nwork + kCUs - 1) / kCUs;
+    const int64_t cus = stream_cu_count(st);
+    const bool short_items = a.T <= 2 * C * a.nseq && nwork >= 2 * cus;
+    const int64_t per = (nwork + cus - 1) / cus;
     items_per_wg = short_items ? (int32_t)(per < 64 ? per : 64) : 0;
   }
   a.per_wg = items_per_wg;
-  const int64_t nblocks = items_per_wg > 0 ? (nwork + items_per_wg - 1) / items_per_wg
-                                           : (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
+  // (with no items the launch still zeroes the rows no sequence covers)
+  const int64_t nblocks = nwork == 0 ? 16
+                          : items_per_wg > 0 ? (nwork + items_per_wg - 1) / items_per_wg
+                                             : (nwork + 15) / 16 * 16;  // the work-id map covers whole groups of 16
   const dim3 grid((unsigned)nblocks), block(kThreads);
-  const bool f16 = q->dtype == GDN_DTYPE_F16, multi = items_per_wg > 0;
-  if (a.kd == KD && a.vd == VD) {
-    if (multi) {
-      if (f16) gdn_chunk_prefill_kernel<true, true, false><<<grid, block, 0, st>>>(a);
-      else gdn_chunk_prefill_kernel<false, true, false><<<grid, block, 0, st>>>(a);
-    } else {
-      if (f16) gdn_chunk_prefill_kernel<true, false, false><<<grid, block, 0, st>>>(a);
-      else gdn_chunk_prefill_kernel<false, false, false><<<grid, block, 0, st>>>(a);
-    }
-  } else {
-    if (multi) {
-      if (f16) gdn_chunk_prefill_kernel<true, true, true><<<grid, block, 0, st>>>(a);
-      else gdn_chunk_prefill_kernel<false, true, true><<<grid, block, 0, st>>>(a);
-    } else {
-      if (f16) gdn_chunk_prefill_kernel<true, false, true><<<grid, block, 0, st>>>(a);
-      else gdn_chunk_prefill_kernel<false, false, true><<<grid, block, 0, st>>>(a);
-    }
-  }
+  const bool f16 = q->dtype == GDN_DTYPE_F16, multi = items_per_wg > 0, pad = a.kd != KD || a.vd != VD;
+  const bool out32 = out->dtype == GDN_DTYPE_F32;  // (q, k, v fp16: checked by the caller)
+#define GDN_PREFILL_LAUNCH(F16, MULTI, PAD, OUT32) \
+  gdn_chunk_prefill_kernel<F16, MULTI, PAD, OUT32><<<grid, block, 0, st>>>(a)
+#define GDN_PREFILL_BY_PAD(F16, MULTI, OUT32)                   \
+  do {                                                           \
+    if (pad) GDN_PREFILL_LAUNCH(F16, MULTI, true, OUT32);        \
+    else GDN_PREFILL_LAUNCH(F16, MULTI, false, OUT32);           \
+  } while (0)
+#define GDN_PREFILL_BY_MULTI(F16, OUT32)                         \
+  do {                                                           \
+    if (multi) GDN_PREFILL_BY_PAD(F16, true, OUT32);             \
+    else GDN_PREFILL_BY_PAD(F16, false, OUT32);                  \
+  } while (0)
+  if (out32) GDN_PREFILL_BY_MULTI(true, true);
+  else if (f16) GDN_PREFILL_BY_MULTI(true, false);
+  else GDN_PREFILL_BY_MULTI(false, false);
+#undef GDN_PREFILL_BY_MULTI
+#undef GDN_PREFILL_BY_PAD
+#undef GDN_PREFILL_LAUNCH
   return hipGetLastError();
 }

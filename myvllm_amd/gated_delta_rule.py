@@ -63,36 +63,43 @@ def chunk_gated_delta_rule(
     return o
 
 
+def chunk_prefill_ex(q, k, v, g, beta, state, idx, cu_seqlens, out, scale, flags=0, items_per_wg=-1,
+                     spin_limit=-1):
+    """``gdn_chunk_prefill_ex``: the prefill with its options (flags
+    ``_lib.PREFILL_*``, the schedule and the bound of the kernel's internal
+    waits; include/gdn_hip.h).  q, k, v bf16 or fp16, last stride 1; out
+    v's dtype, or fp32 for fp16 inputs; nothing is converted or allocated."""
+    dev = _lib.require_device(q, k, v, g, beta, state, idx, cu_seqlens, out)
+    D = _lib.describe
+    rc = _lib.load().gdn_chunk_prefill_ex(
+        D(q), D(k), D(v), D(g), D(beta), D(state), D(idx), D(cu_seqlens), D(out), float(scale), CHUNK_SIZE,
+        int(flags), int(items_per_wg), int(spin_limit), _lib.stream_handle(dev),
+    )
+    _lib.check("gdn_chunk_prefill_ex", rc)
+    return out
+
+
 def _chunk_gated_delta_rule_fp32(q, k, v, g, beta, state, idx, cu_seqlens, scale, out):
-    """fp32 q, k, v through the fp16 kernel.  q and k are rounded to fp16, the
-    MFMA operand type (the reference's kernels run their fp32 dots in tf32,
-    whose 10-bit mantissa fp16 matches); v is split exactly enough into
+    """fp32 q, k, v through the fp16 kernel with fp32 output.  q and k are
+    rounded to fp16, the MFMA operand type (the reference's kernels run their
+    fp32 dots in tf32, whose 10-bit mantissa fp16 matches); v is split into
     v_hi = fp16(v) and v_lo = fp16(v - v_hi) (22 significant bits), and since
-    the recurrence is linear in (state, v) jointly, the kernel runs twice:
-    from the slot's state with v_hi (updating the slot in place) and from a
-    zero state with v_lo (into a temporary); the temporary's final states are
-    added into the slots and o = o_hi + o_lo in fp32.  Two launches; no host
-    synchronisation.  Tokens not covered by any sequence get o = 0."""
+    the recurrence is linear in (state, v) jointly the kernel runs twice: from
+    the slot's state with v_hi, writing o and the final state, then from a
+    zero state with v_lo, adding its o and final state to them
+    (GDN_PREFILL_ZERO_INIT | ACCUM_STATE | ACCUM_OUT).  Two launches, no
+    temporary state, no host synchronisation; padding sequences' slots are
+    not touched.  o keeps the fp32 range; v itself must stay below fp16's
+    65504 in magnitude (v_hi would overflow), as for the 16-bit inputs."""
     dev = v.device
     qh, kh = q.to(torch.float16), k.to(torch.float16)
     v_hi = v.to(torch.float16)
     v_lo = (v - v_hi.float()).to(torch.float16)
-    o_hi = torch.zeros(v.shape, dtype=torch.float16, device=dev)
-    o_lo = torch.zeros(v.shape, dtype=torch.float16, device=dev)
-    chunk_gated_delta_rule(qh, kh, v_hi, g, beta, state, idx, cu_seqlens, scale=scale, out=o_hi)
-    n = cu_seqlens.numel() - 1
-    valid = (idx >= 0) & (idx < state.shape[0])
-    tmp_idx = torch.where(valid, torch.arange(n, dtype=torch.int32, device=dev),
-                          torch.full((n,), -1, dtype=torch.int32, device=dev))
-    tmp = torch.zeros((n,) + tuple(state.shape[1:]), dtype=torch.float32, device=dev)
-    chunk_gated_delta_rule(qh, kh, v_lo, g, beta, tmp, tmp_idx, cu_seqlens, scale=scale, out=o_lo)
-    # (a padding sequence adds its zero temporary to slot 0)
-    state.index_add_(0, torch.where(valid, idx.long(), torch.zeros_like(idx, dtype=torch.long)), tmp)
-    o = torch.add(o_hi.float(), o_lo.float())
-    if out is None:
-        return o
-    out.copy_(o)
-    return out
+    o = torch.empty(v.shape, dtype=torch.float32, device=dev) if out is None else out
+    chunk_prefill_ex(qh, kh, v_hi, g, beta, state, idx, cu_seqlens, o, scale)
+    chunk_prefill_ex(qh, kh, v_lo, g, beta, state, idx, cu_seqlens, o, scale,
+                     flags=_lib.PREFILL_ZERO_INIT | _lib.PREFILL_ACCUM_STATE | _lib.PREFILL_ACCUM_OUT)
+    return o
 
 
 def recurrent_gated_delta_rule(

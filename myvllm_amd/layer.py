@@ -97,17 +97,85 @@ class GatedDeltaNet(nn.Module):
                      (self.conv1d_weight, 1.0 / math.sqrt(self.conv_kernel_size))):
             p.copy_((torch.randn(p.shape, generator=gen) * s).to(p.dtype))
 
+    @staticmethod
+    def _decode_count(T: int, is_prefill, num_decode_tokens) -> int:
+        """Decode tokens of the call from the reference's ``is_prefill`` flag or
+        the mixed-batch ``num_decode_tokens`` (not both, unless they agree)."""
+        if is_prefill is not None and not isinstance(is_prefill, bool):
+            raise TypeError(f"is_prefill must be a bool (got {type(is_prefill).__name__}); "
+                            "pass num_decode_tokens= for a mixed batch")
+        if num_decode_tokens is not None and (isinstance(num_decode_tokens, bool) or
+                                              not isinstance(num_decode_tokens, int)):
+            raise TypeError(f"num_decode_tokens must be an int (got {type(num_decode_tokens).__name__})")
+        if is_prefill is None:
+            n = 0 if num_decode_tokens is None else num_decode_tokens
+        else:
+            n = 0 if is_prefill else T
+            if num_decode_tokens is not None and num_decode_tokens != n:
+                raise ValueError(f"is_prefill={is_prefill} disagrees with num_decode_tokens={num_decode_tokens}")
+        if T >= 0 and not 0 <= n <= T:
+            raise ValueError(f"num_decode_tokens={n} outside [0, {T}]")
+        return n
+
+    def _check_inputs(self, x, cu_seqlens, conv_state_indices, recurrent_state_indices, Tp: int, Td: int) -> int:
+        """Shapes, dtypes and devices of one call; returns the number of prefill sequences."""
+        if x.dim() != 2 or x.shape[1] != self.hidden_size:
+            raise ValueError(f"x must be (T, {self.hidden_size}), got {tuple(x.shape)}")
+        dev = x.device
+        idx_types = (torch.int32, torch.int64)
+        Np = 0
+        if Tp > 0:
+            if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+                raise ValueError("cu_seqlens must be a 1-D tensor of N_prefill + 1 >= 2 offsets")
+            if cu_seqlens.dtype not in idx_types or cu_seqlens.device != dev:
+                raise ValueError(f"cu_seqlens must be int32/int64 on {dev} (got {cu_seqlens.dtype} on "
+                                 f"{cu_seqlens.device})")
+            Np = cu_seqlens.numel() - 1
+        for name, t in (("conv_state_indices", conv_state_indices), ("recurrent_state_indices", recurrent_state_indices)):
+            if not isinstance(t, torch.Tensor) or t.dim() != 1 or t.dtype not in idx_types or t.device != dev:
+                raise ValueError(f"{name} must be a 1-D int32/int64 tensor on {dev}")
+            if t.numel() != Np + Td:
+                raise ValueError(f"{name} has {t.numel()} entries; the call has {Np} prefill sequences and "
+                                 f"{Td} decode tokens")
+        cs, rs = self.conv_state, self.recurrent_state
+        if rs.dim() != 4 or tuple(rs.shape[1:]) != (self.num_v_heads, self.k_head_dim, self.v_head_dim) or \
+                rs.dtype != torch.float32 or rs.device != dev:
+            raise ValueError(f"recurrent_state must be (slots, {self.num_v_heads}, {self.k_head_dim}, "
+                             f"{self.v_head_dim}) fp32 on {dev}; got {tuple(rs.shape)} {rs.dtype}")
+        if cs.dim() != 3 or tuple(cs.shape[1:]) != (self.conv_kernel_size - 1, self.conv_dim) or cs.device != dev:
+            raise ValueError(f"conv_state must be (slots, {self.conv_kernel_size - 1}, {self.conv_dim}) on {dev}; "
+                             f"got {tuple(cs.shape)}")
+        if Td > 0 and (self.conv_kernel_size != 4 or self.k_head_dim != 128 or self.v_head_dim != 128 or
+                       self.num_v_heads // self.num_k_heads not in (1, 2, 4)):
+            raise ValueError("decode tokens need conv width 4, K = V = 128 and Hv / Hk in {1, 2, 4} "
+                             "(the fused decode step)")
+        return Np
+
     def forward(
         self,
         x: torch.Tensor,  # (T, hidden)
         cu_seqlens: torch.Tensor,  # (N_prefill + 1,) over the first T - num_decode_tokens tokens
         conv_state_indices: torch.Tensor,  # (N_prefill + num_decode_tokens,)
         recurrent_state_indices: torch.Tensor,  # (N_prefill + num_decode_tokens,)
-        num_decode_tokens: int = 0,
+        is_prefill: bool | None = None,
+        *,
+        num_decode_tokens: int | None = None,
     ) -> torch.Tensor:
-        T = x.shape[0]
+        """One layer step.  The reference's call form ``forward(x, cu_seqlens,
+        conv_state_indices, recurrent_state_indices, is_prefill)``
+        (``layers/linear_attention.py:77-84``) is accepted as is: ``is_prefill``
+        True makes every token a prefill token, False makes every token one
+        decode step of its own sequence (``cu_seqlens`` is then not read).  A
+        mixed batch passes ``num_decode_tokens`` instead: the prefill tokens
+        first, then that many decode tokens.  Every argument is checked before
+        anything is launched, so a malformed call raises with both caches
+        untouched.  (``cu_seqlens[-1]`` is a device value and is not compared
+        with the prefill token count, which would synchronise the host; the
+        kernels clamp sequences to it and zero the rows no sequence covers.)"""
+        T = x.shape[0] if x.dim() == 2 else -1
+        num_decode_tokens = self._decode_count(T, is_prefill, num_decode_tokens)
         Tp = T - num_decode_tokens
-        Np = cu_seqlens.numel() - 1 if Tp > 0 else 0
+        Np = self._check_inputs(x, cu_seqlens, conv_state_indices, recurrent_state_indices, Tp, num_decode_tokens)
         Hk, Hv, K, V = self.num_k_heads, self.num_v_heads, self.k_head_dim, self.v_head_dim
         proj = x @ self.in_proj.t()
         cz = self.conv_dim + self.v_size

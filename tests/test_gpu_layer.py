@@ -223,3 +223,85 @@ def test_layer_fp32_mixed_batch(dev):
     rel = ((rec[used] - ref_rec[used].double()).norm() / ref_rec[used].double().norm()).item()
     assert rel < 1e-3, rel
     assert torch.allclose(cache.conv_cache[0].cpu().double(), ref_conv.double(), rtol=1e-4, atol=1e-5)
+
+
+def test_layer_reference_call_form(dev):
+    """The reference's positional call ``layer(x, cu_seqlens,
+    conv_state_indices, recurrent_state_indices, is_prefill)``
+    (layers/linear_attention.py:77-84): True is an all-prefill call, False an
+    all-decode call; each equals, bit for bit, the same batch given by
+    ``num_decode_tokens``, from the same caches."""
+    layer = GatedDeltaNet(HID, HK, HV, K, V, device=dev)
+    layer.init_random(seed=11)
+    g = torch.Generator().manual_seed(12)
+    cache = LinearAttentionCache(1, 8, 4, K, V, HK, HV, torch.bfloat16, dev, conv_dtype=torch.float32)
+    cache.conv_cache[0].copy_(torch.randn(cache.conv_cache[0].shape, generator=g))
+    cache.recurrent_cache[0].copy_(torch.randn(cache.recurrent_cache[0].shape, generator=g) * 0.1)
+    conv0, rec0 = cache.conv_cache[0].clone(), cache.recurrent_cache[0].clone()
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    cu = cu_from_lengths([90, 38]).to(dev)
+    idx = torch.tensor([5, 2], dtype=torch.int32, device=dev)
+    x = torch.randn(128, HID, generator=g).bfloat16().to(dev)
+    results = []
+    for kw in (dict(), dict(num_decode_tokens=0)):
+        cache.conv_cache[0].copy_(conv0)
+        cache.recurrent_cache[0].copy_(rec0)
+        out = layer(x, cu, idx, idx, True, **kw) if not kw else layer(x, cu, idx, idx, **kw)
+        torch.cuda.synchronize()
+        results.append((out.cpu(), cache.conv_cache[0].cpu(), cache.recurrent_cache[0].cpu()))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+    xd = torch.randn(3, HID, generator=g).bfloat16().to(dev)
+    idx3 = torch.tensor([1, 6, 3], dtype=torch.int32, device=dev)
+    results = []
+    for form in ("flag", "count"):
+        cache.conv_cache[0].copy_(conv0)
+        cache.recurrent_cache[0].copy_(rec0)
+        if form == "flag":
+            out = layer(xd, cu, idx3, idx3, False)
+        else:
+            out = layer(xd, cu[:1], idx3, idx3, num_decode_tokens=3)
+        torch.cuda.synchronize()
+        results.append((out.cpu(), cache.conv_cache[0].cpu(), cache.recurrent_cache[0].cpu()))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bad", ["idx_len", "bool_count", "count_range", "cu_dtype", "flag_mismatch", "rec_dtype"])
+def test_layer_rejects_bad_calls_before_launching(dev, bad):
+    """A malformed call raises before any kernel runs: both caches stay bit
+    for bit what they were (the last check used to come from the decode
+    step's own validation, after the prefill had written the cache)."""
+    layer = GatedDeltaNet(HID, HK, HV, K, V, device=dev)
+    layer.init_random(seed=13)
+    g = torch.Generator().manual_seed(14)
+    cache = LinearAttentionCache(1, 6, 4, K, V, HK, HV, torch.bfloat16, dev, conv_dtype=torch.float32)
+    cache.conv_cache[0].copy_(torch.randn(cache.conv_cache[0].shape, generator=g))
+    cache.recurrent_cache[0].copy_(torch.randn(cache.recurrent_cache[0].shape, generator=g) * 0.1)
+    conv0, rec0 = cache.conv_cache[0].clone(), cache.recurrent_cache[0].clone()
+    layer.conv_state, layer.recurrent_state = cache.layer(0)
+    x = torch.randn(70, HID, generator=g).bfloat16().to(dev)
+    cu = cu_from_lengths([40, 28]).to(dev)
+    idx = torch.tensor([0, 4, 2, 5], dtype=torch.int32, device=dev)
+    kw = dict(num_decode_tokens=2)
+    if bad == "idx_len":
+        idx = idx[:3]
+    elif bad == "bool_count":
+        kw = dict(num_decode_tokens=True)
+    elif bad == "count_range":
+        kw = dict(num_decode_tokens=71)
+    elif bad == "cu_dtype":
+        cu = cu.float()
+    elif bad == "flag_mismatch":
+        args = (x, cu, idx, idx, True)
+        kw = dict(num_decode_tokens=2)
+    elif bad == "rec_dtype":
+        layer.recurrent_state = cache.recurrent_cache[0].double()
+    with pytest.raises((ValueError, TypeError)):
+        if bad == "flag_mismatch":
+            layer(*args, **kw)
+        else:
+            layer(x, cu, idx, idx, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.conv_cache[0], conv0)
+    assert torch.equal(cache.recurrent_cache[0], rec0)

@@ -4,22 +4,31 @@ import torch
 
 from conftest import assert_out_close, assert_state_close
 from myvllm_amd import chunk_gated_delta_rule, chunk_gated_delta_rule_fwd, recurrent_gated_delta_rule
+from myvllm_amd.gated_delta_rule import chunk_prefill_ex
 from myvllm_amd.workloads import cu_from_lengths, prefill_32k_case, prefill_case
 from oracle.gdn import chunk_gated_delta_rule_ref, recurrent_gated_delta_rule_ref
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(case, dev, idx=None, cu=None, beta=None):
+def _run(case, dev, idx=None, cu=None, beta=None, items_per_wg=None, spin_limit=None):
+    """The op on the GPU and the oracle on the CPU.  With items_per_wg or
+    spin_limit the call goes through gdn_chunk_prefill_ex with that schedule
+    (-1: the launcher's choice) and wait bound (-1: the default)."""
     idx = case.idx if idx is None else idx
     cu = case.cu if cu is None else cu
     beta = case.beta if beta is None else beta
     st_ref = case.state.clone()
     o_ref = chunk_gated_delta_rule_ref(case.q, case.k, case.v, case.g, beta, st_ref, idx, cu)
     st = case.state.to(dev)
-    o = chunk_gated_delta_rule(
-        case.q.to(dev), case.k.to(dev), case.v.to(dev), case.g.to(dev), beta.to(dev), st, idx.to(dev), cu.to(dev)
-    )
+    args = (case.q.to(dev), case.k.to(dev), case.v.to(dev), case.g.to(dev), beta.to(dev), st, idx.to(dev), cu.to(dev))
+    if items_per_wg is None and spin_limit is None:
+        o = chunk_gated_delta_rule(*args)
+    else:
+        o = torch.full(case.v.shape, float("nan"), dtype=case.v.dtype, device=dev)
+        chunk_prefill_ex(*args, o, case.q.shape[-1] ** -0.5,
+                         items_per_wg=-1 if items_per_wg is None else items_per_wg,
+                         spin_limit=-1 if spin_limit is None else spin_limit)
     torch.cuda.synchronize()
     return o.cpu(), st.cpu(), o_ref, st_ref
 
@@ -181,11 +190,12 @@ def test_prefill_32k_full(dev):
     _check(case, o, st, o_ref, st_ref)
 
 
-@pytest.mark.parametrize("key", ["norm1", "norm8", "norm64", "spiky8"])
+@pytest.mark.parametrize("key", ["norm1", "norm8", "norm64", "norm128", "spiky8", "spiky128"])
 def test_prefill_key_magnitudes(dev, key):
-    """Keys that are not unit vectors: L2 norms 1, 8 and 64 in random
-    directions, and norm-8 keys whose mass sits in one coordinate (|k_i| near
-    8), under weak decay over many chunks.  beta is divided by |k|^2 so the
+    """Keys that are not unit vectors: L2 norms 1, 8, 64 and 128 (the largest
+    the C ABI accepts) in random directions, and norm-8 and norm-128 keys whose
+    mass sits in one coordinate (|k_i| near 8 and 128), under weak decay over
+    many chunks.  beta is divided by |k|^2 so the
     delta rule stays contractive (1 - beta |k|^2 in (0, 1)), as the unit-key
     recurrence is.  The state then scales like 1 / |k|, so outputs and states
     are compared after multiplying by |k| (the bars are stated for unit-scale
@@ -194,8 +204,8 @@ def test_prefill_key_magnitudes(dev, key):
     case = prefill_case([700, 300, 64], seed=21, num_slots=4, Hk=2, Hv=4, g_scale=0.05)
     gen = torch.Generator().manual_seed(22)
     k = torch.nn.functional.normalize(torch.randn(case.k.shape, generator=gen), dim=-1)
-    if key == "spiky8":
-        rho = 8.0
+    if key.startswith("spiky"):
+        rho = float(key[5:])
         k = k * 0.05
         hot = torch.randint(0, k.shape[-1], k.shape[:2], generator=gen)
         k.scatter_(-1, hot[..., None], 1.0)
@@ -267,16 +277,16 @@ def _stream_batch():
     return case, idx
 
 
-@pytest.mark.parametrize("per_wg", ["0", "1", "3", "64"])
-def test_prefill_item_stream(dev, monkeypatch, per_wg):
+@pytest.mark.parametrize("per_wg", [0, 1, 3, 64])
+def test_prefill_item_stream(dev, per_wg):
     """The same batch with one item (sequence, v-head) per workgroup, longest
-    first (0), and with 1, 3 and 64 consecutive items per workgroup walked as
-    one chunk stream, whose producers stage the next item's first chunks while
-    the state waves finish the current item."""
+    first (0), and with runs of about 1, 3 and 64 items per workgroup (dealt
+    by their token counts) walked as one chunk stream, whose producers stage
+    the next item's first chunks while the state waves finish the current
+    item."""
     case, idx = _stream_batch()
-    monkeypatch.setenv("GDN_PREFILL_ITEMS_PER_WG", per_wg)
     print(f"prefill item stream: {per_wg} items per workgroup, {case.tokens} tokens", flush=True)
-    o, st, o_ref, st_ref = _run(case, dev, idx=idx)
+    o, st, o_ref, st_ref = _run(case, dev, idx=idx, items_per_wg=per_wg)
     _check(case, o, st, o_ref, st_ref, idx=idx)
 
 
@@ -291,14 +301,12 @@ def test_prefill_many_short_sequences_auto_stream(dev):
     _check(case, o, st, o_ref, st_ref)
 
 
-def test_prefill_wait_give_up_poisons_the_stream(dev, monkeypatch):
+def test_prefill_wait_give_up_poisons_the_stream(dev):
     """With several items per workgroup a wait that gives up poisons every
     item of the workgroup from that point: all rows NaN here (the limit is 0
     from the start), no state slot written."""
     case, idx = _stream_batch()
-    monkeypatch.setenv("GDN_PREFILL_ITEMS_PER_WG", "8")
-    monkeypatch.setenv("GDN_PREFILL_SPIN_LIMIT", "0")
-    o, st, _, _ = _run(case, dev, idx=idx)
+    o, st, _, _ = _run(case, dev, idx=idx, items_per_wg=8, spin_limit=0)
     pad = torch.zeros(case.tokens, dtype=torch.bool)
     pad[int(case.cu[7]):int(case.cu[8])] = True
     assert torch.isnan(o[~pad].float()).all()
@@ -306,19 +314,17 @@ def test_prefill_wait_give_up_poisons_the_stream(dev, monkeypatch):
     assert torch.equal(st, case.state)
 
 
-def test_prefill_wait_give_up_poisons_the_item(dev, monkeypatch):
+def test_prefill_wait_give_up_poisons_the_item(dev):
     """The kernel's waits between its wave roles are bounded; one that gives
     up must not pass as a plausible answer.  Forced from the host (spin limit
     0, so every wait gives up at once and every wave still runs to its end):
     every output row is NaN and no state slot is written.  With the default
-    limit restored the same call is correct again."""
+    limit the same call is correct again."""
     case = prefill_case([200, 70], seed=25, num_slots=3, Hk=2, Hv=4)
-    monkeypatch.setenv("GDN_PREFILL_SPIN_LIMIT", "0")
-    o, st, _, _ = _run(case, dev)
+    o, st, _, _ = _run(case, dev, spin_limit=0)
     assert torch.isnan(o.float()).all()
     assert torch.equal(st, case.state)
-    monkeypatch.delenv("GDN_PREFILL_SPIN_LIMIT")
-    o, st, o_ref, st_ref = _run(case, dev)
+    o, st, o_ref, st_ref = _run(case, dev, spin_limit=-1)
     _check(case, o, st, o_ref, st_ref)
 
 

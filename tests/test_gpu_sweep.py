@@ -42,15 +42,13 @@ def _prefill_cfg(i: int) -> dict:
     return dict(lengths=[_length(r, 300) for _ in range(r.randint(1, 6))], Hk=Hk, Hv=Hk * r.choice([1, 2, 4]),
                 K=r.choice([128, 64, 8 * r.randint(1, 16)]), V=r.choice([128, 64, 8 * r.randint(1, 16)]),
                 dtype=r.choice(DTYPES), g_scale=r.choice([0.05, 1.0, 3.0]), pad=r.random() < 0.3,
-                i64=r.random() < 0.3, per_wg=r.choice(["", "", "1", "3", "64"]))
+                i64=r.random() < 0.3, per_wg=r.choice([None, None, 1, 3, 64]))
 
 
 @pytest.mark.parametrize("i", range(40))
-def test_sweep_prefill(dev, monkeypatch, i):
+def test_sweep_prefill(dev, i):
     c = _prefill_cfg(i)
     print(f"sweep prefill {i}: {c}", flush=True)
-    if c["per_wg"]:
-        monkeypatch.setenv("GDN_PREFILL_ITEMS_PER_WG", c["per_wg"])
     N = len(c["lengths"])
     case = prefill_case(c["lengths"], seed=i, num_slots=N + 2, Hk=c["Hk"], Hv=c["Hv"], K=c["K"], V=c["V"],
                         dtype=c["dtype"], g_scale=c["g_scale"])
@@ -59,7 +57,7 @@ def test_sweep_prefill(dev, monkeypatch, i):
         idx[N // 2] = -1
     if c["i64"]:
         idx, cu = idx.long(), cu.long()
-    o, st, o_ref, st_ref = prefill_run(case, dev, idx=idx, cu=cu)
+    o, st, o_ref, st_ref = prefill_run(case, dev, idx=idx, cu=cu, items_per_wg=c["per_wg"])
     prefill_check(case, o, st, o_ref, st_ref, idx=idx)
     if c["pad"]:
         s, e = int(cu[N // 2]), int(cu[N // 2 + 1])
