@@ -96,8 +96,9 @@ typedef struct gdn_tensor {
  *   state_indices : (B,) i32|i64
  *   out    : (B, Hv, V)  bf16|f16|f32, last stride 1
  * Per (b, h): S <- e^g S; d = beta (v - S^T k); S += k d^T; o = S^T (scale q).
- * Head dims: K and V multiples of 8 up to 128 (64 x 64 and 128 x 128 have
- * their own kernels; other shapes run zero-padded in the 128 x 128 one).
+ * Head dims: K and V multiples of 8 up to 256 (64 x 64, 128 x 128 and
+ * 256 x 256 have their own kernels; other shapes run zero-padded in the
+ * 128 x 128 one, or the 256 x 256 one when either dim exceeds 128).
  */
 int gdn_recurrent_step(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                        const gdn_tensor* g, const gdn_tensor* beta, gdn_tensor* state,
@@ -236,9 +237,12 @@ int causal_conv1d_varlen_qknorm(const gdn_tensor* x, const gdn_tensor* weight, g
 /*
  * Gated RMSNorm of the GDN output <- RMSNormGated, layers/norm.py:44-58 (applied
  * per v-head at layers/linear_attention.py:121):
- *   out = x * rsqrt(mean(x^2) + eps) * weight * silu(gate), fp32 math.
- * x, gate, out: (T, H, 128), same dtype, unit inner stride, 16-byte aligned
- * rows; weight: (128,) fp32, bf16 or fp16.
+ *   out = x * rsqrt(mean(x^2) + eps) * weight * silu(gate), fp32 math, the
+ *   mean over the last dim (as the reference's, for any normalized_shape).
+ * x, gate, out: (T, H, N), same dtype (fp32, bf16 or fp16), unit inner
+ * stride, any N >= 1; weight: (N,) shared by the heads or (H, N) one row per
+ * head, fp32, bf16 or fp16, unit inner stride.  N = 128 with a shared weight
+ * and 16-byte aligned rows (the layer's v-heads) takes a vectorised kernel.
  */
 int gdn_rms_norm_gated(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* weight, gdn_tensor* out,
                        float eps, void* stream);

@@ -11,6 +11,7 @@ from .full_attention import (
     paged_flash_attention_decode,
     paged_flash_attention_prefill,
 )
+from .norm import RMSNormGated
 from .gated_delta_rule import (
     chunk_gated_delta_rule,
     chunk_gated_delta_rule_fwd,
@@ -28,4 +29,5 @@ __all__ = [
     "chunk_gated_delta_rule_fwd",
     "gated_delta_net_decode_step",
     "recurrent_gated_delta_rule",
+    "RMSNormGated",
 ]

@@ -22,7 +22,7 @@ hipError_t causal_conv1d_varlen_launch(const gdn_tensor* x, const gdn_tensor* w,
                                        const gdn_tensor* idx, const gdn_tensor* cu, gdn_tensor* out,
                                        int64_t norm_ch, hipStream_t st);
 hipError_t gdn_rms_norm_gated_launch(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* w,
-                                     gdn_tensor* out, float eps, hipStream_t st);
+                                     gdn_tensor* out, float eps, bool fast, hipStream_t st);
 hipError_t gdn_gating_launch(const gdn_tensor* ga, const gdn_tensor* gb, const gdn_tensor* A_log,
                              const gdn_tensor* dt_bias, gdn_tensor* g, gdn_tensor* beta, hipStream_t st);
 hipError_t causal_conv1d_step_launch(const gdn_tensor* x, const gdn_tensor* w, gdn_tensor* cs,
@@ -141,8 +141,9 @@ int check_recurrent(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* 
     // multiples of 8 up to 128 (16-byte rows); below 128 the kernel pads with zeros
     if (K < 8 || K > 128 || K % 8 != 0 || V < 8 || V > 128 || V % 8 != 0) return GDN_ERR_HEAD_DIM;
   } else {
-    // multiples of 8 up to 128 (64 x 64 and 128 x 128 have their own kernels, others run zero-padded)
-    if (K < 8 || K > 128 || K % 8 != 0 || V < 8 || V > 128 || V % 8 != 0) return GDN_ERR_HEAD_DIM;
+    // multiples of 8 up to 256 (64 x 64, 128 x 128 and 256 x 256 have their own
+    // kernels, others run zero-padded in the 128 x 128 or the 256 x 256 one)
+    if (K < 8 || K > 256 || K % 8 != 0 || V < 8 || V > 256 || V % 8 != 0) return GDN_ERR_HEAD_DIM;
   }
 
   // strides
@@ -401,19 +402,24 @@ GDN_EXPORT int gdn_rms_norm_gated(const gdn_tensor* x, const gdn_tensor* gate, c
                                   gdn_tensor* out, float eps, void* stream) {
   GDN_TRY(check_desc(x, 3));
   GDN_TRY(check_desc(gate, 3));
-  GDN_TRY(check_desc(weight, 1));
+  if (!weight) return GDN_ERR_NULL;
+  GDN_TRY(check_desc(weight, weight->ndim == 2 ? 2 : 1));
   GDN_TRY(check_desc(out, 3));
   for (int i = 0; i < 3; ++i)
     if (gate->shape[i] != x->shape[i] || out->shape[i] != x->shape[i]) return GDN_ERR_SHAPE;
-  if (weight->shape[0] != x->shape[2]) return GDN_ERR_SHAPE;
-  if (x->shape[2] != 128) return GDN_ERR_HEAD_DIM;
+  const int64_t H = x->shape[1], N = x->shape[2];
+  // weight: one row of N shared by every head, or one row per head (H, N)
+  if (weight->ndim == 1 ? weight->shape[0] != N : (weight->shape[0] != H || weight->shape[1] != N))
+    return GDN_ERR_SHAPE;
   if (!is_float(x->dtype) || out->dtype != x->dtype || gate->dtype != x->dtype || !is_float(weight->dtype))
     return GDN_ERR_DTYPE;
-  if (x->stride[2] != 1 || gate->stride[2] != 1 || out->stride[2] != 1 || weight->stride[0] != 1)
+  if (x->stride[2] != 1 || gate->stride[2] != 1 || out->stride[2] != 1 || weight->stride[weight->ndim - 1] != 1)
     return GDN_ERR_STRIDE;
-  if (numel(x) > 0 && (!vec_ok(x, 16) || !vec_ok(gate, 16) || !vec_ok(out, 16))) return GDN_ERR_ALIGN;
-  if (x->shape[0] * x->shape[1] > kMaxGrid * 16) return GDN_ERR_RANGE;
-  return launch_rc(gdn_rms_norm_gated_launch(x, gate, weight, out, eps, reinterpret_cast<hipStream_t>(stream)));
+  if (x->shape[0] * H > kMaxGrid * 4) return GDN_ERR_RANGE;
+  // 128-element rows with one weight row and 16-byte aligned rows: the fast kernel
+  const bool fast = N == 128 && weight->ndim == 1 &&
+                    (numel(x) == 0 || (vec_ok(x, 16) && vec_ok(gate, 16) && vec_ok(out, 16)));
+  return launch_rc(gdn_rms_norm_gated_launch(x, gate, weight, out, eps, fast, reinterpret_cast<hipStream_t>(stream)));
 }
 
 GDN_EXPORT int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log, const gdn_tensor* dt_bias,

@@ -221,13 +221,17 @@ hipError_t launch_heads(const RecurrentArgs& a, int64_t nitems, hipStream_t st) 
   return hipGetLastError();
 }
 
-// 128 x 128 and 64 x 64 have their own instantiations; any other head dims
-// (multiples of 8 up to 128) run zero-padded in the 128 x 128 one.
+// 128 x 128, 64 x 64 and 256 x 256 have their own instantiations; any other
+// head dims (multiples of 8) run zero-padded in the 128 x 128 one when both
+// are at most 128, else in the 256 x 256 one (one row group per wave there:
+// 64 lanes x 4 columns span a 256-wide row).
 template <typename TIn>
 hipError_t launch_dims(const RecurrentArgs& a, int K, int V, int64_t nitems, hipStream_t st) {
   if (K == 128 && V == 128) return launch_heads<TIn, 128, 128>(a, nitems, st);
   if (K == 64 && V == 64) return launch_heads<TIn, 64, 64>(a, nitems, st);
-  return launch_heads<TIn, 128, 128, true>(a, nitems, st);
+  if (K <= 128 && V <= 128) return launch_heads<TIn, 128, 128, true>(a, nitems, st);
+  if (K == 256 && V == 256) return launch_heads<TIn, 256, 256>(a, nitems, st);
+  return launch_heads<TIn, 256, 256, true>(a, nitems, st);
 }
 
 }  // namespace

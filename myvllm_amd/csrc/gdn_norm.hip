@@ -1,10 +1,13 @@
 // Gated RMSNorm of the GDN output, per v-head:
 //   y = x rsqrt(mean x^2 + eps) w silu(gate)      (fp32 math, output in x's dtype)
 // as RMSNormGated (layers/norm.py:44-58 of yuyifanbupt/myvllm) applies it to
-// o and z at layers/linear_attention.py:121.  A row is one (token, head) of
-// 128 elements: 16 lanes x 8 elements (16-byte accesses), the sum of squares
-// over a DPP row; each 16-lane group takes kRowsPer rows with all their loads
-// in flight at once.
+// o and z at layers/linear_attention.py:121.  A row is one (token, head).
+// Rows of 128 elements (the layer's v-heads) take the fast kernel: 16 lanes
+// x 8 elements (16-byte accesses), the sum of squares over a DPP row; each
+// 16-lane group takes kRowsPer rows with all their loads in flight at once.
+// Any other row length N (the reference takes any normalized_shape and
+// reduces over its last dim) runs one wave per row, elements strided over the
+// lanes, with a weight of N values or one row of N per head.
 //
 // Also the layer's gates, g = -exp(A_log) softplus(a + dt_bias) and
 // beta = sigmoid(b) (layers/linear_attention.py:89-90), in fp32, one launch.
@@ -15,7 +18,8 @@ namespace {
 struct NormArgs {
   const void* x; const void* gate; const void* w; void* out;
   int64_t x_s0, x_s1, g_s0, g_s1, o_s0, o_s1;
-  int64_t rows, H;
+  int64_t rows, H, N;
+  int64_t w_sh;  // weight stride per head (0: one weight row shared by all heads)
   int32_t w_dtype;
   float eps;
 };
@@ -65,6 +69,34 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gated_kernel(NormArgs a) {
   }
 }
 
+// Any row length: one wave per row, four rows per workgroup; the row is read
+// twice (the second pass hits the cache), the sum of squares reduced over the
+// wave with lane shuffles.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rms_norm_gated_any_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // (whole waves: the shuffles below see every lane of the wave)
+  const int64_t t = row / a.H, h = row % a.H;
+  const T* x = reinterpret_cast<const T*>(a.x) + t * a.x_s0 + h * a.x_s1;
+  const T* gt = reinterpret_cast<const T*>(a.gate) + t * a.g_s0 + h * a.g_s1;
+  T* out = reinterpret_cast<T*>(a.out) + t * a.o_s0 + h * a.o_s1;
+  const int64_t w0 = h * a.w_sh;
+  float ss = 0.f;
+  for (int64_t c = lane; c < a.N; c += 64) {
+    const float v = to_f32(x[c]);
+    ss = fmaf(v, v, ss);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  const float r = rsqrtf(ss / (float)a.N + a.eps);
+  for (int64_t c = lane; c < a.N; c += 64) {
+    const float g = to_f32(gt[c]);
+    const float silu = g / (1.f + __expf(-g));
+    out[c] = from_f32<T>(to_f32(x[c]) * r * load_scalar_f32(a.w, w0 + c, a.w_dtype) * silu);
+  }
+}
+
 struct GateArgs {
   const void* ga; const void* gb; const void* A_log; const void* dt_bias;
   float* g; float* beta;
@@ -88,9 +120,10 @@ __global__ __launch_bounds__(kThreads) void gdn_gating_kernel(GateArgs a) {
 
 }  // namespace
 
-// Called by the validated C entry point in gdn_capi.cpp (head dim 128).
+// Called by the validated C entry point in gdn_capi.cpp.  fast: 128-element
+// rows, one shared weight row, 16-byte aligned rows (checked there).
 hipError_t gdn_rms_norm_gated_launch(const gdn_tensor* x, const gdn_tensor* gate, const gdn_tensor* w,
-                                     gdn_tensor* out, float eps, hipStream_t st) {
+                                     gdn_tensor* out, float eps, bool fast, hipStream_t st) {
   NormArgs a;
   a.x = x->data; a.gate = gate->data; a.w = w->data; a.out = out->data;
   a.x_s0 = x->stride[0]; a.x_s1 = x->stride[1];
@@ -98,9 +131,20 @@ hipError_t gdn_rms_norm_gated_launch(const gdn_tensor* x, const gdn_tensor* gate
   a.o_s0 = out->stride[0]; a.o_s1 = out->stride[1];
   a.rows = x->shape[0] * x->shape[1];
   a.H = x->shape[1];
+  a.N = x->shape[2];
+  a.w_sh = w->ndim == 2 ? w->stride[0] : 0;
   a.w_dtype = w->dtype;
   a.eps = eps;
-  if (a.rows == 0) return hipSuccess;
+  if (a.rows == 0 || a.N == 0) return hipSuccess;
+  if (!fast) {
+    const dim3 grid((unsigned)((a.rows + kThreads / 64 - 1) / (kThreads / 64)));
+    switch (x->dtype) {
+      case GDN_DTYPE_BF16: rms_norm_gated_any_kernel<bf16_t><<<grid, dim3(kThreads), 0, st>>>(a); break;
+      case GDN_DTYPE_F16: rms_norm_gated_any_kernel<f16_t><<<grid, dim3(kThreads), 0, st>>>(a); break;
+      default: rms_norm_gated_any_kernel<float><<<grid, dim3(kThreads), 0, st>>>(a); break;
+    }
+    return hipGetLastError();
+  }
   const int64_t blocks = (a.rows + kRows - 1) / kRows;
   switch (x->dtype) {
     case GDN_DTYPE_BF16: rms_norm_gated_kernel<bf16_t><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(a); break;

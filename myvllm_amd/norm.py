@@ -13,16 +13,46 @@ from . import _lib
 
 
 def rms_norm_gated(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """x, gate: (T, H, 128) (or any (..., H, 128) view with unit inner stride); weight: (128,)."""
+    """Normalises over the last dim N of x (any shape (..., N)); gate has x's
+    shape; weight is (N,), or (H, N) for x of shape (..., H, N) (the
+    reference's weight of normalized_shape broadcast over the leading dims)."""
     dev = _lib.require_device(x, gate, weight)
+    if gate.shape != x.shape:
+        raise ValueError(f"gate shape {tuple(gate.shape)} != x shape {tuple(x.shape)}")
     shape = x.shape
-    x3 = x.reshape(-1, shape[-2], shape[-1]) if x.dim() != 3 else x
-    g3 = gate.reshape(x3.shape) if gate.shape != x3.shape else gate
+    if weight.dim() == 2:
+        x3 = x.reshape(-1, shape[-2], shape[-1])
+    elif x.dim() >= 3:
+        x3 = x.reshape(-1, shape[-2], shape[-1])
+    else:
+        x3 = x.reshape(-1, 1, shape[-1])
+    g3 = gate.reshape(x3.shape)
+    if x3.stride(-1) != 1:
+        x3 = x3.contiguous()
+    if g3.stride(-1) != 1:
+        g3 = g3.contiguous()
     out = torch.empty(x3.shape, dtype=x.dtype, device=dev)
     D = _lib.describe
     rc = _lib.load().gdn_rms_norm_gated(D(x3), D(g3), D(weight), D(out), float(eps), _lib.stream_handle(dev))
     _lib.check("gdn_rms_norm_gated", rc)
     return out.reshape(shape)
+
+
+class RMSNormGated(torch.nn.Module):
+    """Drop-in for ``RMSNormGated`` (``layers/norm.py:44-58``): same
+    constructor arguments, ``weight`` parameter and ``forward(x, gate)``, on
+    the HIP kernel (no torch.compile)."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-6, device=None) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(normalized_shape, device=device))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        w = self.weight
+        if w.dim() > 2:
+            raise ValueError("normalized_shape of more than two dims is not supported")
+        return rms_norm_gated(x, gate, w, self.variance_epsilon)
 
 
 def gdn_gating(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor):

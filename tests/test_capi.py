@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "gdn_hip.h")
 
 ERR = {"NULL": -1, "NDIM": -2, "SHAPE": -3, "DTYPE": -4, "STRIDE": -5, "HEADS": -6, "HEAD_DIM": -7, "CHUNK": -8,
-       "ALIGN": -9, "CONV_WIDTH": -10, "RANGE": -11, "SCRATCH": -12}
+       "ALIGN": -9, "CONV_WIDTH": -10, "RANGE": -11, "SCRATCH": -12, "ARG": -13}
 
 
 def declared_functions():
@@ -87,7 +87,8 @@ def _call_prefill(a, cu, chunk=64):
         (lambda a: a.update(q=torch.zeros(2, 2, 256, dtype=torch.bfloat16)[:, :, ::2]), "STRIDE"),
         (lambda a: a.update(state=torch.zeros(3, 4, 128, 256)[..., :128]), "STRIDE"),
         (lambda a: a.update(**_recurrent_args(K=100, V=96)), "HEAD_DIM"),
-        (lambda a: a.update(**_recurrent_args(K=136, V=128)), "HEAD_DIM"),
+        (lambda a: a.update(**_recurrent_args(K=264, V=128)), "HEAD_DIM"),
+        (lambda a: a.update(**_recurrent_args(K=128, V=260)), "HEAD_DIM"),
     ],
 )
 def test_recurrent_step_validation(mutate, code):
@@ -123,6 +124,34 @@ def test_prefill_validation():
     d["idx"] = torch.zeros(2, dtype=torch.int32)
     d["g"] = torch.zeros(10, 4, dtype=torch.bfloat16)
     assert _call_prefill(d, cu) == ERR["DTYPE"]
+
+
+def _call_prefill_ex(a, cu, flags=0, per_wg=-1, spin=-1):
+    lib = _lib.load()
+    return lib.gdn_chunk_prefill_ex(D(a["q"]), D(a["k"]), D(a["v"]), D(a["g"]), D(a["beta"]), D(a["state"]),
+                                    D(a["idx"]), D(cu), D(a["out"]), 1.0, 64, flags, per_wg, spin, None)
+
+
+@cpu_only
+def test_prefill_ex_validation():
+    """gdn_chunk_prefill_ex: unknown flags and out-of-range options are
+    GDN_ERR_ARG; an fp32 out only for fp16 q/k/v, and ACCUM_OUT only with it;
+    everything else is checked as for gdn_chunk_prefill."""
+    a = _recurrent_args(B=10)
+    a["idx"] = torch.zeros(2, dtype=torch.int32)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    assert _call_prefill_ex(a, cu, flags=8) == ERR["ARG"]
+    assert _call_prefill_ex(a, cu, per_wg=65) == ERR["ARG"]
+    assert _call_prefill_ex(a, cu, per_wg=-2) == ERR["ARG"]
+    assert _call_prefill_ex(a, cu, spin=-2) == ERR["ARG"]
+    assert _call_prefill_ex(a, cu, spin=(1 << 22) + 1) == ERR["ARG"]
+    assert _call_prefill_ex(a, cu, flags=_lib.PREFILL_ACCUM_OUT) == ERR["DTYPE"]  # bf16 out
+    a["out"] = torch.zeros(10, 4, 128, dtype=torch.float32)
+    assert _call_prefill_ex(a, cu) == ERR["DTYPE"]  # fp32 out needs fp16 inputs
+    b = _recurrent_args(B=10, dtype=torch.float16)
+    b["idx"] = torch.zeros(2, dtype=torch.int32)
+    b["out"] = torch.zeros(10, 4, 100, dtype=torch.float32)
+    assert _call_prefill_ex(b, cu) == ERR["SHAPE"]
     e = _recurrent_args(B=10)
     e["idx"] = torch.zeros(2, dtype=torch.int32)
     e["v"] = torch.zeros(10, 4, 130, dtype=torch.bfloat16)[:, :, 1:129]  # 2-byte offset: misaligned
@@ -367,3 +396,19 @@ def test_paged_decode_noalloc_rejects_more_than_the_static_scratch():
     a["splits"] = 1  # no partials: nothing needs the scratch
     assert _lib.load().paged_attention_decode_workspace_size(B, Hq, Dh, 1) == 0
 
+
+
+@cpu_only
+def test_rms_norm_gated_validation():
+    """Any row length N; weight (N,) or (H, N); shapes must agree."""
+    lib = _lib.load()
+    x = torch.zeros(3, 2, 72, dtype=torch.bfloat16)
+
+    def call(x, g, w, o):
+        return lib.gdn_rms_norm_gated(D(x), D(g), D(w), D(o), 1e-6, None)
+
+    assert call(x, x, torch.ones(71), x) == ERR["SHAPE"]
+    assert call(x, x, torch.ones(3, 72), x) == ERR["SHAPE"]  # per-head weight with 3 rows for 2 heads
+    assert call(x, torch.zeros(3, 2, 72), torch.ones(72), x) == ERR["DTYPE"]
+    assert call(x, x, torch.ones(72, 2)[:, 0], x) == ERR["STRIDE"]
+    assert call(x, x, torch.ones(1, 2, 72), x) == ERR["NDIM"]

@@ -34,10 +34,13 @@ def test_decode_small(dev, K):
     assert torch.equal(st[untouched], case.state[untouched])
 
 
-@pytest.mark.parametrize("K, V", [(32, 32), (128, 64), (64, 128), (96, 40), (8, 8)])
+@pytest.mark.parametrize("K, V", [(32, 32), (128, 64), (64, 128), (96, 40), (8, 8), (256, 256), (192, 256),
+                                  (256, 136), (136, 72), (8, 256)])
 def test_decode_other_head_dims(dev, K, V):
-    """Head dims other than 64 x 64 and 128 x 128 (multiples of 8 up to 128)
-    run zero-padded in the 128 x 128 kernel; a padding slot among them."""
+    """Head dims other than 64 x 64 and 128 x 128 (multiples of 8) run
+    zero-padded in the 128 x 128 kernel, or in the 256 x 256 one when either
+    exceeds 128 (the reference's decode kernel has no head-dim cap,
+    ops/gated_delta_rule/fused_recurrent_gdn.py:51-58); a padding slot among them."""
     case = decode_case(B=7, num_slots=12, seed=K + V, Hk=2, Hv=4, K=K, V=V)
     idx = case.idx.clone()
     idx[3] = -1

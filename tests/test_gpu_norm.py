@@ -27,6 +27,32 @@ def test_rms_norm_gated(dev, dtype):
         assert_out_close(out, ref)
 
 
+@pytest.mark.parametrize("N,per_head,dtype", [(64, False, torch.bfloat16), (72, False, torch.float16),
+                                               (1000, False, torch.float32), (3, True, torch.bfloat16),
+                                               (128, True, torch.bfloat16), (256, False, torch.bfloat16)])
+def test_rms_norm_gated_any_row_length(dev, N, per_head, dtype):
+    """Any normalized_shape (the reference's RMSNormGated takes one and
+    reduces over its last dim, layers/norm.py:44-58): row lengths other than
+    128, odd ones included, with one shared weight row or one per head, through
+    the nn.Module drop-in as well."""
+    from myvllm_amd.norm import RMSNormGated
+
+    g = torch.Generator().manual_seed(N)
+    x = (torch.randn(29, 5, N, generator=g) * 3).to(dtype)
+    z = torch.randn(29, 5, N, generator=g).to(dtype)
+    w = torch.rand((5, N) if per_head else (N,), generator=g) + 0.5
+    ref = rms_norm_gated_ref(x, z, w)
+    out = rms_norm_gated(x.to(dev), z.to(dev), w.to(dev)).cpu()
+    if dtype == torch.float32:
+        assert torch.allclose(out, ref, rtol=1e-5, atol=1e-6)
+    else:
+        assert_out_close(out, ref)
+    m = RMSNormGated((5, N) if per_head else (N,), eps=1e-6, device=dev)
+    with torch.no_grad():
+        m.weight.copy_(w)
+    assert torch.equal(m(x.to(dev), z.to(dev)).cpu(), out)
+
+
 def test_rms_norm_gated_empty(dev):
     x = torch.zeros(0, 4, 128, dtype=torch.bfloat16, device=dev)
     assert rms_norm_gated(x, x, torch.ones(128, device=dev)).shape == (0, 4, 128)
