@@ -77,24 +77,40 @@ def _traffic(kernel: str):
 
 
 def _cpu_model() -> str:
-    """lscpu's model name (/proc/cpuinfo where lscpu is missing)."""
+    """The host CPU's full identification: /proc/cpuinfo's model name, lscpu's
+    model and BIOS model names where they differ from it, and the family /
+    model / stepping numbers (lscpu alone prints only "AMD EPYC" on some hosts)."""
     import subprocess
 
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
-    except (OSError, subprocess.SubprocessError):
-        pass
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if fields:
+                        break
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                    fields[k] = v
     except OSError:
         pass
-    return "unknown"
+    lscpu = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                lscpu.setdefault(k, v)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    name = fields.get("model name") or lscpu.get("Model name") or "unknown"
+    extra = [f"{label} {lscpu[k]}" for k, label in (("Model name", "lscpu"), ("BIOS Model name", "BIOS"))
+             if lscpu.get(k) and lscpu[k] != name]
+    if "cpu family" in fields:
+        extra.append(f"family {fields['cpu family']} model {fields.get('model', '?')} "
+                     f"stepping {fields.get('stepping', '?')}")
+    return name + (f" ({'; '.join(extra)})" if extra else "")
 
 
 def _cpu_info() -> dict:
@@ -354,6 +370,45 @@ def bench_prefill_short(dev, steps, warmup, cpu_budget):
                                             f"first {n} of the {case.idx.numel()} sequences ({Ts} tokens), "
                                             "fp32 chunked (C=64) torch restatement")
     return res
+
+
+def bench_prefill_skewed(dev, steps, warmup, cpu_budget):
+    """A chunked-prefill scheduler's batch with one long prompt chunk among
+    many short ones: 384 sequences of 64 tokens and one of 16,384 (40,960
+    tokens), Hk 16 / Hv 32, d 128.  The launcher takes the many-items
+    schedule (two chunks or fewer per sequence on average); its runs are
+    priced by tokens, so the long sequence's 32 items spread over workgroups.
+    The same batch is also timed with one item per workgroup, longest first
+    (gdn_chunk_prefill_ex, items_per_wg = 0), for comparison."""
+    from myvllm_amd import chunk_gated_delta_rule
+    from myvllm_amd.gated_delta_rule import chunk_prefill_ex
+    from myvllm_amd.workloads import prefill_case
+
+    lengths = [64] * 384 + [16384]
+    case = prefill_case(lengths, seed=7, num_slots=len(lengths))
+    T = case.tokens
+    q, k, v, g, beta, state, idx, cu = (t.to(dev) for t in (case.q, case.k, case.v, case.g, case.beta,
+                                                             case.state, case.idx, case.cu))
+    o = torch.empty(v.shape, dtype=v.dtype, device=dev)
+
+    def step(_):
+        chunk_gated_delta_rule(q, k, v, g, beta, state, idx, cu, out=o)
+
+    def step_one_item(_):
+        chunk_prefill_ex(q, k, v, g, beta, state, idx, cu, o, DK ** -0.5, items_per_wg=0)
+
+    tm = _time_gpu(step, steps, warmup)
+    tm1 = _time_gpu(step_one_item, steps, warmup)
+    nbytes = prefill_bytes(case)
+    gbs = nbytes / (tm.median_ms * 1e-3) / 1e9
+    return {
+        "tokens": T, "sequences": len(lengths), **tm.fields(),
+        "tokens_per_s": T / (tm.step_ms * 1e-3),
+        "one_item_per_workgroup_kernel_ms": tm1.median_ms,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None, "bytes_per_launch": nbytes,
+                     "kernel": "gdn_chunk_prefill_kernel"},
+    }
 
 
 def bench_decode(dev, steps, warmup, cpu_budget):
@@ -774,7 +829,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="all",
-                    help="all, or a comma-separated list of prefill, prefill_short, decode, conv, conv_update, "
+                    help="all, or a comma-separated list of prefill, prefill_short, prefill_skewed, decode, conv, "
+                         "conv_update, "
                          "decode_fused, "
                          "layer, attn_prefill, attn_paged_prefill, attn_decode, hbm_copy")
     ap.add_argument("--settle-ms", type=float, default=300.0,
@@ -800,8 +856,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    known = {"prefill", "prefill_short", "decode", "conv", "conv_update", "decode_fused", "layer", "attn_prefill",
-             "attn_paged_prefill", "attn_decode", "hbm_copy"}
+    known = {"prefill", "prefill_short", "prefill_skewed", "decode", "conv", "conv_update", "decode_fused", "layer",
+             "attn_prefill", "attn_paged_prefill", "attn_decode", "hbm_copy"}
     chosen = set(args.workload.split(","))
     if not chosen <= (known | {"all"}):
         print(f"unknown workload(s): {sorted(chosen - known - {'all'})}", file=sys.stderr)
@@ -815,6 +871,11 @@ def main():
         parts["prefill_short"] = bench_prefill_short(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# prefill_short: {parts['prefill_short']['kernel_ms'] * 1e3:.1f} us/launch "
               f"({parts['prefill_short']['roofline']['achieved']:.0f} GB/s)", file=sys.stderr, flush=True)
+    if want("prefill_skewed"):
+        parts["prefill_skewed"] = bench_prefill_skewed(dev, min(args.steps, 20), min(args.warmup, 5), args.cpu_seconds)
+        print(f"# prefill_skewed: {parts['prefill_skewed']['kernel_ms'] * 1e3:.1f} us/launch (one item per "
+              f"workgroup: {parts['prefill_skewed']['one_item_per_workgroup_kernel_ms'] * 1e3:.1f})",
+              file=sys.stderr, flush=True)
     if want("decode"):
         parts["decode"] = bench_decode(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# decode: {parts['decode']['kernel_ms'] * 1e3:.1f} us/launch", file=sys.stderr, flush=True)

@@ -152,6 +152,9 @@ int gdn_chunk_prefill(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor
  *   serve fp32 q/k/v: the recurrence is linear in (state, v), so with
  *   v = v_hi + v_lo (fp16 each) one call with v_hi and fp32 out and a second
  *   with v_lo, ZERO_INIT | ACCUM_STATE | ACCUM_OUT give the result for v.
+ *   q and k are then rounded to fp16 (the MFMA operand type): against fp32
+ *   q/k the final state holds a norm-wise bar (1e-3 relative), the
+ *   elementwise 1e-3 |ref| + 1e-6 only against the same rounded q and k.
  *   items_per_wg: -1 lets the launcher choose the schedule; 0 is one
  *     (sequence, v-head) item per workgroup, longest sequence first; 1..64
  *     deals the items in runs priced by their tokens to ceil(N Hv /
