@@ -160,6 +160,21 @@ def check(fn: str, code: int) -> None:
         raise GdnError(fn, code, strerror(code))
 
 
+def vec16(t: torch.Tensor) -> torch.Tensor:
+    """t itself when the kernels can read it with 16-byte vector accesses (unit
+    inner stride, 16-byte aligned data and outer strides), else a contiguous
+    copy: the reference passes every stride to its kernels, so any strided
+    input is accepted, at the cost of a copy when it is misaligned."""
+    es = t.element_size()
+    if t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((t.stride(i) * es) % 16 == 0 for i in range(t.dim() - 1)):
+        return t
+    return t.contiguous()
+
+
+def vec16_ok(t: torch.Tensor) -> bool:
+    return vec16(t) is t
+
+
 def require_device(*tensors: torch.Tensor) -> torch.device:
     """All tensors must live on one HIP device (the kernels dereference the pointers)."""
     dev = None

@@ -33,8 +33,7 @@ def causal_conv1d_fn(
     to x's dtype.
     """
     dev = _lib.require_device(x, weight, conv_state, conv_state_indices, cu_seqlens)
-    if x.stride(-1) != 1:
-        x = x.contiguous()
+    x = _lib.vec16(x)
     o = torch.empty(x.shape, dtype=x.dtype, device=dev)
     D = _lib.describe
     lib = _lib.load()

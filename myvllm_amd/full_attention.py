@@ -21,6 +21,21 @@ import torch
 
 from . import _lib
 
+
+def _out_for(out, shape, dtype, dev):
+    """The tensor the kernel writes: `out` itself when it has 16-byte aligned
+    rows, else a temporary copied into `out` afterwards (_finish)."""
+    if out is not None and _lib.vec16_ok(out):
+        return out
+    return torch.empty(shape, dtype=dtype, device=dev)
+
+
+def _finish(out, o):
+    if out is not None and o is not out:
+        out.copy_(o)
+        return out
+    return o
+
 _DECODE_MIN_SPLIT_KEYS = 256
 _DECODE_TARGET_WAVES = 2048
 _DECODE_MAX_SPLITS = 256
@@ -52,17 +67,17 @@ def flash_attention_prefill(
     if q.shape[1] != num_heads or k.shape[1] != num_kv_heads or q.shape[2] != head_dim or v.shape[2] != head_v_dim:
         raise ValueError("q/k/v shapes disagree with num_heads/num_kv_heads/head_dim/head_v_dim")
     dev = _lib.require_device(q, k, v, cu_seqlens)
+    q, k, v = _lib.vec16(q), _lib.vec16(k), _lib.vec16(v)
     if max_seqlen is None:
         max_seqlen = _max_seqlen(cu_seqlens)
-    if out is None:
-        out = torch.empty(q.shape[0], q.shape[1], head_v_dim, dtype=q.dtype, device=dev)
+    o = _out_for(out, (q.shape[0], q.shape[1], head_v_dim), q.dtype, dev)
     D = _lib.describe
     rc = _lib.load().flash_attention_varlen(
-        D(q), D(k), D(v), D(cu_seqlens), D(out), int(max_seqlen), float(scale), int(bool(is_causal)),
+        D(q), D(k), D(v), D(cu_seqlens), D(o), int(max_seqlen), float(scale), int(bool(is_causal)),
         _lib.stream_handle(dev),
     )
     _lib.check("flash_attention_varlen", rc)
-    return out
+    return _finish(out, o)
 
 
 def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int, capacity: int) -> int:
@@ -104,15 +119,15 @@ def paged_flash_attention_decode(
     n_ws = lib.paged_attention_decode_workspace_size(B, Hq, Dh, int(num_splits))
     if n_ws > 0:
         ws = torch.empty(n_ws, dtype=torch.float32, device=dev)
-    if out is None:
-        out = torch.empty(B, Hq, v_cache.shape[-1], dtype=q.dtype, device=dev)
+    q, k_cache, v_cache = _lib.vec16(q), _lib.vec16(k_cache), _lib.vec16(v_cache)
+    o = _out_for(out, (B, Hq, v_cache.shape[-1]), q.dtype, dev)
     D = _lib.describe
     rc = lib.paged_attention_decode(
-        D(q), D(k_cache), D(v_cache), D(block_tables), D(context_lens), D(out),
+        D(q), D(k_cache), D(v_cache), D(block_tables), D(context_lens), D(o),
         D(ws) if ws is not None else None, int(num_splits), float(scale), _lib.stream_handle(dev),
     )
     _lib.check("paged_attention_decode", rc)
-    return out
+    return _finish(out, o)
 
 
 def paged_flash_attention_decode_noalloc(
@@ -167,12 +182,12 @@ def paged_flash_attention_prefill(
     dev = _lib.require_device(q, k_cache, v_cache, page_block_tables, context_lens, cu_seqlens)
     if max_seqlen is None:
         max_seqlen = _max_seqlen(cu_seqlens)
-    if out is None:
-        out = torch.empty(q.shape[0], q.shape[1], v_cache.shape[-1], dtype=q.dtype, device=dev)
+    q, k_cache, v_cache = _lib.vec16(q), _lib.vec16(k_cache), _lib.vec16(v_cache)
+    o = _out_for(out, (q.shape[0], q.shape[1], v_cache.shape[-1]), q.dtype, dev)
     D = _lib.describe
     rc = _lib.load().paged_attention_prefill(
-        D(q), D(k_cache), D(v_cache), D(page_block_tables), D(context_lens), D(cu_seqlens), D(out),
+        D(q), D(k_cache), D(v_cache), D(page_block_tables), D(context_lens), D(cu_seqlens), D(o),
         int(max_seqlen), float(scale), _lib.stream_handle(dev),
     )
     _lib.check("paged_attention_prefill", rc)
-    return out
+    return _finish(out, o)

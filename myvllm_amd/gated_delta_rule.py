@@ -42,7 +42,7 @@ def chunk_gated_delta_rule(
     """Prefill over packed varlen sequences (reference ``gated_delta_rule.py:31-66``);
     ``out`` (optional) receives o in place of a new tensor."""
     dev = _lib.require_device(q, k, v, g, beta, recurrent_state, recurrent_state_indices, cu_seqlens)
-    q, k, v = _lastdim_contiguous(q), _lastdim_contiguous(k), _lastdim_contiguous(v)
+    q, k, v = _lib.vec16(q), _lib.vec16(k), _lib.vec16(v)
     if g.dtype != torch.float32:
         g = g.float()
     if scale is None:
@@ -52,7 +52,8 @@ def chunk_gated_delta_rule(
             raise ValueError(f"q, k and v must share one dtype (got {q.dtype}, {k.dtype}, {v.dtype})")
         return _chunk_gated_delta_rule_fp32(q, k, v, g, beta, recurrent_state, recurrent_state_indices, cu_seqlens,
                                             scale, out)
-    o = torch.empty(v.shape, dtype=v.dtype, device=dev) if out is None else out
+    # (an out the kernel cannot write with 16-byte stores is filled through a temporary)
+    o = torch.empty(v.shape, dtype=v.dtype, device=dev) if out is None or not _lib.vec16_ok(out) else out
     lib = _lib.load()
     D = _lib.describe
     rc = lib.gdn_chunk_prefill(
@@ -60,6 +61,9 @@ def chunk_gated_delta_rule(
         float(scale), CHUNK_SIZE, _lib.stream_handle(dev),
     )
     _lib.check("gdn_chunk_prefill", rc)
+    if out is not None and o is not out:
+        out.copy_(o)
+        return out
     return o
 
 
@@ -95,10 +99,13 @@ def _chunk_gated_delta_rule_fp32(q, k, v, g, beta, state, idx, cu_seqlens, scale
     qh, kh = q.to(torch.float16), k.to(torch.float16)
     v_hi = v.to(torch.float16)
     v_lo = (v - v_hi.float()).to(torch.float16)
-    o = torch.empty(v.shape, dtype=torch.float32, device=dev) if out is None else out
+    o = torch.empty(v.shape, dtype=torch.float32, device=dev) if out is None or not _lib.vec16_ok(out) else out
     chunk_prefill_ex(qh, kh, v_hi, g, beta, state, idx, cu_seqlens, o, scale)
     chunk_prefill_ex(qh, kh, v_lo, g, beta, state, idx, cu_seqlens, o, scale,
                      flags=_lib.PREFILL_ZERO_INIT | _lib.PREFILL_ACCUM_STATE | _lib.PREFILL_ACCUM_OUT)
+    if out is not None and o is not out:
+        out.copy_(o)
+        return out
     return o
 
 
