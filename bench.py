@@ -871,7 +871,7 @@ def main():
         parts["prefill_short"] = bench_prefill_short(dev, args.steps, args.warmup, args.cpu_seconds)
         print(f"# prefill_short: {parts['prefill_short']['kernel_ms'] * 1e3:.1f} us/launch "
               f"({parts['prefill_short']['roofline']['achieved']:.0f} GB/s)", file=sys.stderr, flush=True)
-    if want("prefill_skewed"):
+    if "prefill_skewed" in chosen:  # (named explicitly only: it shares the short-sequence kernel)
         parts["prefill_skewed"] = bench_prefill_skewed(dev, min(args.steps, 20), min(args.warmup, 5), args.cpu_seconds)
         print(f"# prefill_skewed: {parts['prefill_skewed']['kernel_ms'] * 1e3:.1f} us/launch (one item per "
               f"workgroup: {parts['prefill_skewed']['one_item_per_workgroup_kernel_ms'] * 1e3:.1f})",

@@ -36,6 +36,7 @@ def _finish(out, o):
         return out
     return o
 
+
 _DECODE_MIN_SPLIT_KEYS = 256
 _DECODE_TARGET_WAVES = 2048
 _DECODE_MAX_SPLITS = 256
@@ -67,9 +68,11 @@ def flash_attention_prefill(
     if q.shape[1] != num_heads or k.shape[1] != num_kv_heads or q.shape[2] != head_dim or v.shape[2] != head_v_dim:
         raise ValueError("q/k/v shapes disagree with num_heads/num_kv_heads/head_dim/head_v_dim")
     dev = _lib.require_device(q, k, v, cu_seqlens)
-    q, k, v = _lib.vec16(q), _lib.vec16(k), _lib.vec16(v)
     if max_seqlen is None:
         max_seqlen = _max_seqlen(cu_seqlens)
+    if head_dim not in _KERNEL_HEAD_DIMS or head_v_dim != head_dim:
+        return _padded_prefill(q, k, v, cu_seqlens, scale, head_dim, head_v_dim, is_causal, max_seqlen, out)
+    q, k, v = _lib.vec16(q), _lib.vec16(k), _lib.vec16(v)
     o = _out_for(out, (q.shape[0], q.shape[1], head_v_dim), q.dtype, dev)
     D = _lib.describe
     rc = _lib.load().flash_attention_varlen(
@@ -78,6 +81,24 @@ def flash_attention_prefill(
     )
     _lib.check("flash_attention_varlen", rc)
     return _finish(out, o)
+
+
+_KERNEL_HEAD_DIMS = (64, 128, 256)
+
+
+def _padded_prefill(q, k, v, cu_seqlens, scale, head_dim, head_v_dim, is_causal, max_seqlen, out):
+    """Head dims the kernel has no instantiation for (the vision tower's
+    1152 / 16 = 72, ``models/qwen/vision.py:18``, ``configs/qwen3_5.py:11``,
+    ``:16``) run zero-padded to the next of 64, 128 and 256: zero dims add
+    nothing to q.k and give zero output columns, which are dropped.  The
+    padded copies cost one pass over q, k and v."""
+    Dp = next((d for d in _KERNEL_HEAD_DIMS if d >= max(head_dim, head_v_dim)), None)
+    if Dp is None:
+        raise ValueError(f"head dims {head_dim}/{head_v_dim} above {_KERNEL_HEAD_DIMS[-1]} are not supported")
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dp - t.shape[-1]))
+    o = flash_attention_prefill(pad(q), pad(k), pad(v), cu_seqlens, scale, q.shape[1], k.shape[1], Dp, Dp, is_causal,
+                                max_seqlen=max_seqlen)
+    return _finish(out, o[..., :head_v_dim]) if out is not None else o[..., :head_v_dim]
 
 
 def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int, capacity: int) -> int:

@@ -187,3 +187,16 @@ def test_paged_decode_layer_workload(dev):
     print(f"attn decode workload B=256 keys={int(case.context_lens.sum())}", flush=True)
     out = _decode(case, dev, None)
     assert_attn_close(out, _decode_ref(case))
+
+
+@pytest.mark.parametrize("Dh, causal", [(72, False), (72, True), (40, True), (200, False)])
+def test_varlen_prefill_other_head_dims(dev, Dh, causal):
+    """Head dims without a kernel instantiation, such as the vision tower's
+    1152 / 16 = 72 (models/qwen/vision.py:18, non-causal), run zero-padded to
+    the next of 64, 128 and 256; against the oracle at the unpadded dim."""
+    case = attn_varlen_case([100, 37, 1], seed=Dh, Hq=16, Hkv=16, D=Dh)
+    print(f"varlen head dim {Dh} causal={causal}", flush=True)
+    out = _varlen(case, dev, causal)
+    ref = flash_attention_prefill_ref(case.q, case.k, case.v, case.cu, case.scale, is_causal=causal)
+    assert out.shape == case.q.shape
+    assert_attn_close(out, ref)
