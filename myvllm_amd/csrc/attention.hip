@@ -147,13 +147,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // output rows no sequence covers are zero, as the reference allocates o
-  // zero-filled (ops/full_attention.py:467)
-  zero_uncovered_rows<(int)sizeof(T)>(a.o, a.o_st, a.o_sh, a.Hq, D, a.cu, a.cu64, a.nseq, a.T,
-                                      blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z),
-                                      (int64_t)gridDim.x * gridDim.y * gridDim.z, tid, 256);
   const int64_t n = blockIdx.z;
-  if (n >= a.nseq) return;
   const int R = a.Hq / a.Hkv, gh = a.gh, qsubs = 4 / gh, groups = R / gh;
   const int kvh = blockIdx.y / groups;
   const int head = kvh * R + (blockIdx.y % groups) * gh + (w % gh);
@@ -778,9 +772,15 @@ PagedTable paged_table(const gdn_tensor* tab, const gdn_tensor* kc) {
 template <typename T, int D, int BN, bool PAGED>
 hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hipStream_t st) {
   const int qsubs = 4 / a.gh;
-  // (at least one workgroup, which zeroes the rows no sequence covers)
-  const int64_t qblocks = max_len > 0 ? (max_len + 32 * qsubs - 1) / (32 * qsubs) : 1;
-  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)(nseq > 0 ? nseq : 1));
+  // output rows no sequence covers are zero, as the reference allocates o
+  // zero-filled (ops/full_attention.py:467); a kernel of its own, launched
+  // first (a call inside the attention kernel changed its register allocation
+  // and cost it about a fifth of its speed)
+  zero_uncovered_rows_kernel<(int)sizeof(T)><<<dim3(64), dim3(256), 0, st>>>(a.o, a.o_st, a.o_sh, a.Hq, D, a.cu,
+                                                                             a.cu64, a.nseq, a.T);
+  if (nseq <= 0 || max_len <= 0) return hipGetLastError();
+  const int64_t qblocks = (max_len + 32 * qsubs - 1) / (32 * qsubs);
+  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)nseq);
   if (!PAGED)
     hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 0>), grid, dim3(256), 0, st, a);
   else if (a.tab.page % 16 == 0)

@@ -210,6 +210,16 @@ __device__ __attribute__((noinline)) void zero_uncovered_rows(void* out, int64_t
   }
 }
 
+// The same as a kernel of its own, for kernels whose register allocation a
+// call would disturb: launched just before them on their stream (256 threads
+// per workgroup, any grid).
+template <int ES>
+__global__ __launch_bounds__(256) void zero_uncovered_rows_kernel(void* out, int64_t s0, int64_t s1, int64_t H,
+                                                                  int64_t Dv, const void* cu, bool cu64,
+                                                                  int64_t nseq, int64_t T) {
+  zero_uncovered_rows<ES>(out, s0, s1, H, Dv, cu, cu64, nseq, T, blockIdx.x, gridDim.x, threadIdx.x, 256);
+}
+
 
 // Sum over the 16 lanes of a DPP row, on every lane of the row (quad swaps,
 // then the half-row and row mirrors).
