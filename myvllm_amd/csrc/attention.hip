@@ -122,6 +122,20 @@ GDN_DEVICE const char* kv_row(const KvSource& s, const PagedTable& tb, int64_t n
 // PG: 0 packed rows, 1 paged (any page size: a table lookup per row),
 // 2 paged with a page size that is a multiple of 16 (one lookup per 16 rows,
 // through the scalar cache, so the data loads do not wait on vector loads)
+// Workgroup id -> (sequence, query tile): tiles of tile_len queries, laid out
+// sequence after sequence over the tiles that exist (no workgroup of a
+// padded grid exits idle).  Out of line, so that the lookup's registers and
+// barriers leave the kernel's own allocation alone.
+struct SeqTile {
+  int64_t seq, tile;
+};
+__device__ __attribute__((always_inline)) SeqTile attn_tile_lookup(const void* cu, bool cu64, int64_t nseq, int64_t T,
+                                                              int tile_len, int64_t target, int32_t* lds) {
+  SeqTile r;
+  find_seq_tile<256>(cu, cu64, nseq, T, tile_len, target, r.seq, r.tile, lds);
+  return r;
+}
+
 template <typename T, int D, int BN, int PG>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   constexpr bool PAGED = PG != 0;
@@ -147,16 +161,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t n = blockIdx.z;
   const int R = a.Hq / a.Hkv, gh = a.gh, qsubs = 4 / gh, groups = R / gh;
-  const int kvh = blockIdx.y / groups;
-  const int head = kvh * R + (blockIdx.y % groups) * gh + (w % gh);
+  // Workgroup order: sequence after sequence, a sequence's query tiles last
+  // first, the head groups of a tile innermost.  The dispatcher deals
+  // consecutive workgroups to its 32 queues (8 XCDs x 4 shader engines, 8
+  // CUs each) in turn, so every sequence spreads over all of them, and a
+  // sequence's workgroups run together and share its K/V rows in L2.
+  __shared__ int32_t lookup[8];
+  const int hg = a.Hq / gh;  // head groups
+  const SeqTile st = attn_tile_lookup(a.cu, a.cu64, a.nseq, a.T, 32 * qsubs, blockIdx.x / hg, lookup);
+  if (st.seq < 0) return;
+  const int64_t n = st.seq;
+  const int y = (int)(blockIdx.x % hg);
+  const int kvh = y / groups;
+  const int head = kvh * R + (y % groups) * gh + (w % gh);
 
   int64_t s0, s1;
   seq_range(a.cu, a.cu64, n, a.T, s0, s1);
   const int64_t len = s1 - s0;
-  const int64_t qb = (int64_t)(gridDim.x - 1 - blockIdx.x) * 32 * qsubs;  // last query blocks first
-  if (qb >= len) return;
+  const int64_t ntile = (len + 32 * qsubs - 1) / (32 * qsubs);
+  const int64_t qb = (ntile - 1 - st.tile) * 32 * qsubs;  // last query tiles first
 
   int64_t Lk, off;
   if (PAGED) {
@@ -779,8 +803,9 @@ hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hi
   zero_uncovered_rows_kernel<(int)sizeof(T)><<<dim3(64), dim3(256), 0, st>>>(a.o, a.o_st, a.o_sh, a.Hq, D, a.cu,
                                                                              a.cu64, a.nseq, a.T);
   if (nseq <= 0 || max_len <= 0) return hipGetLastError();
-  const int64_t qblocks = (max_len + 32 * qsubs - 1) / (32 * qsubs);
-  const dim3 grid((unsigned)qblocks, (unsigned)(a.Hq / a.gh), (unsigned)nseq);
+  // query tiles: at most T / tile_len + one partial tile per sequence
+  const int64_t tiles = a.T / (32 * qsubs) + nseq;
+  const dim3 grid((unsigned)(tiles * (a.Hq / a.gh)));
   if (!PAGED)
     hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 0>), grid, dim3(256), 0, st, a);
   else if (a.tab.page % 16 == 0)
