@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_027_533_104,
-    "gdn_chunk_prefill_kernel/short": 3_863_819_344,
-    "gdn_recurrent_step_kernel": 1_083_438_368,
-    "causal_conv1d_varlen_kernel": 666_028_480,
-    "causal_conv1d_step_kernel": 59_315_840,
-    "gdn_decode_fused_kernel": 1_131_465_152,
-    "attn_prefill_kernel": 1_333_012_872,
-    "attn_decode_kernel": 1_268_914_840,  # with its combine kernel
-    "attn_paged_prefill_kernel": 1_187_020_896,
+    "gdn_chunk_prefill_kernel": 1_025_839_424,
+    "gdn_chunk_prefill_kernel/short": 3_851_921_920,
+    "gdn_recurrent_step_kernel": 1_083_302_704,
+    "causal_conv1d_varlen_kernel": 666_028_800,
+    "causal_conv1d_step_kernel": 59_316_832,
+    "gdn_decode_fused_kernel": 1_131_380_288,
+    "attn_prefill_kernel": 938_025_712,
+    "attn_decode_kernel": 1_268_935_544,  # with its combine kernel
+    "attn_paged_prefill_kernel": 821_463_360,
 }
 
 
