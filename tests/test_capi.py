@@ -37,6 +37,23 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.gdn_abi_version() == _lib.ABI_VERSION
 
 
+def test_library_reads_no_environment():
+    """Schedules and wait bounds are call arguments (gdn_chunk_prefill_ex),
+    not environment variables: the built library imports no getenv, so a
+    stray variable in a serving process cannot change a call."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm is not installed")
+    undefined = subprocess.run([nm, "-D", "--undefined-only", _lib.LIB_PATH], check=True, capture_output=True,
+                               text=True).stdout
+    names = {line.split()[-1].split("@")[0] for line in undefined.splitlines() if line.strip()}
+    assert "hipLaunchKernel" in names  # (the listing is the library's own imports)
+    assert not names & {"getenv", "secure_getenv", "__secure_getenv"}, names
+
+
 def test_header_error_codes_match():
     text = open(HEADER).read()
     for name, code in ERR.items():
