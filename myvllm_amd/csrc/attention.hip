@@ -203,27 +203,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   const int col = lane & 31, hh = lane >> 5;
   const int64_t qi = q0 + col;
   const bool qvalid = qi < len;
+  // (loaded unconditionally from a clamped row, so the loads stay in flight
+  // while tile 0's K/V loads are issued; rows past the sequence are zeroed
+  // where the fragments are staged, below)
   v8 qf[NKS];
   {
     const T* qp = reinterpret_cast<const T*>(a.q) + (s0 + (qvalid ? qi : 0)) * a.q_st + (int64_t)head * a.q_sh + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      qf[s] = qvalid ? *reinterpret_cast<const v8*>(qp + 16 * s) : v8{};
-    }
+    for (int s = 0; s < NKS; ++s) qf[s] = *reinterpret_cast<const v8*>(qp + 16 * s);
   }
   // the softmax below assumes c > 0: a negative scale is folded into q (an
   // exact sign flip), a zero scale is q = 0 with c = 1 (equal weights)
   float c = a.c;
-  if (c <= 0.f) {
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) qf[s] = c < 0.f ? -qf[s] : v8{};
-    c = c < 0.f ? -c : 1.f;
-  }
   T* const qw = qs + (QL ? w * 32 * LDK : 0);  // this wave's query rows (only the wave reads them)
-  if constexpr (QL) {
+  auto stage_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) *reinterpret_cast<v8*>(qw + col * LDK + 16 * s + 8 * hh) = qf[s];
-  }
+    for (int s = 0; s < NKS; ++s) qf[s] = qvalid ? qf[s] : v8{};
+    if (c <= 0.f) {
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) qf[s] = c < 0.f ? -qf[s] : v8{};
+      c = c < 0.f ? -c : 1.f;
+    }
+    if constexpr (QL) {
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) *reinterpret_cast<v8*>(qw + col * LDK + 16 * s + 8 * hh) = qf[s];
+    }
+  };
 
   // staging of a K/V tile: global rows -> registers (rows past kend read as
   // zero, so a tile past the range loads nothing) -> LDS
@@ -462,6 +467,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   // and tile t + 2 is in flight: two register sets (A: even tiles, B: odd)
   uint4 kA[NLD], vA[NLD], kB[NLD], vB[NLD];
   load_tile(0, kA, vA);
+  stage_q();  // (waits for the query loads with tile 0's loads in flight)
   store_tile(0, kA, vA);
   load_tile(1, kB, vB);
   load_tile(2, kA, vA);
@@ -479,7 +485,34 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 
   const float lt = lsum + __shfl_xor(lsum, 32);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qvalid) {
+  if constexpr (QL) {
+    // O goes out through the wave's own query rows in LDS (no longer read):
+    // each lane writes its 4-dim pieces of its query's row, then reads back
+    // 16-byte row pieces, so that one store instruction covers two whole
+    // output rows (512 contiguous bytes each) instead of 32 rows x 16 bytes
+#pragma unroll
+    for (int d = 0; d < NDT; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        v4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (T)(oacc[d][4 * g + e] * inv);
+        *reinterpret_cast<v4*>(qw + col * LDK + 32 * d + 8 * g + 4 * hh) = ov;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int cpos = lane & (CH - 1), rsub = lane / CH;  // 16-byte piece of a row, row within the pass
+    constexpr int RPP = 64 / CH;                           // rows per pass
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += RPP) {
+      const int r = r0 + rsub;
+      const v8 ov = *reinterpret_cast<const v8*>(qw + r * LDK + 8 * cpos);
+      if (q0 + r < len)
+        *reinterpret_cast<v8*>(reinterpret_cast<T*>(a.o) + (s0 + q0 + r) * a.o_st + (int64_t)head * a.o_sh +
+                               8 * cpos) = ov;
+    }
+  } else if (qvalid) {
     T* op = reinterpret_cast<T*>(a.o) + (s0 + qi) * a.o_st + (int64_t)head * a.o_sh + 4 * hh;
 #pragma unroll
     for (int d = 0; d < NDT; ++d)
