@@ -120,8 +120,8 @@ GDN_DEVICE const char* kv_row(const KvSource& s, const PagedTable& tb, int64_t n
 // (double buffered, the next tile prefetched into registers) and shared by
 // the four waves.
 // PG: 0 packed rows, 1 paged (any page size: a table lookup per row),
-// 2 paged with a page size that is a multiple of 16 (one lookup per 16 rows,
-// through the scalar cache, so the data loads do not wait on vector loads)
+// 2 / 3 paged with a page size that is a multiple of 16 and an int32 / int64
+// block table (one lookup per 16 rows, a tile ahead, 32-bit arithmetic)
 // Workgroup id -> (sequence, query tile): tiles of tile_len queries, laid out
 // sequence after sequence over the tiles that exist (no workgroup of a
 // padded grid exits idle).  Out of line, so that the lookup's registers and
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       (void*)(a.v.base + s0 * a.v.st + kvh * a.v.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.v.st), 0x00020000);
   constexpr int NG = BN / 16;  // 16-row groups of a tile
   static_assert(CH >= 8 && 64 % CH == 0, "a wave's rows of a tile lie in one 16-row group");
-  // PG == 2: each 16-row group of a tile lies in one page.  Its block id is a
+  // PG 2, 3: each 16-row group of a tile lies in one page.  Its block id is a
   // vector load issued one tile ahead, before the previous tile's data loads,
   // so waiting for it leaves those data loads in flight (a scalar load would
   // be waited for at once, its value forming the addresses, and that wait
@@ -256,21 +256,29 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   uint32_t idlo[NG], idhi[NG];  // raw block ids of the next tile to load
   bool idin[NG];                // its groups lie inside the range and the table
   uint32_t slots[NG];           // their first page slot
-  const uint32_t gpp = PG == 2 ? (uint32_t)a.tab.page / 16 : 1u;  // 16-row groups per page
+  constexpr bool G16 = PG >= 2, T64 = PG == 3;  // 16-row groups per page lookup; int64 table
+  const uint32_t gpp = G16 ? (uint32_t)a.tab.page / 16 : 1u;  // 16-row groups per page
   uint32_t gcol = 0, grem = 0;  // table column and group within the page of the next group
+  // (G16) this sequence's row of the block table as 32-bit words; the table
+  // has columns, and key positions (columns x page), block ids and block
+  // strides fit 32 bits (the launcher takes the per-row path otherwise)
+  const uint32_t* trow = G16 ? reinterpret_cast<const uint32_t*>(a.tab.table) + (T64 ? 2 : 1) * (n * a.tab.row_stride)
+                             : nullptr;
+  const uint32_t kend32 = (uint32_t)kend;
   auto load_ids = [&](int t, uint32_t* lo, uint32_t* hi, bool* in, uint32_t* sl) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const uint32_t j0 = (uint32_t)t * BN + 16 * g;
-      in[g] = j0 < kend && gcol < a.tab.cols;
+      in[g] = j0 < kend32 && gcol < a.tab.cols;
       // (the index goes through a vector register so the loads stay vector loads)
-      int64_t e = in[g] ? n * a.tab.row_stride + gcol : 0;
+      uint32_t e = in[g] ? gcol : 0u;
       asm volatile("" : "+v"(e));
-      const uint32_t* tp = reinterpret_cast<const uint32_t*>(a.tab.table);
-      lo[g] = hi[g] = 0u;
-      if (a.tab.cols > 0) {
-        lo[g] = tp[a.tab.is64 ? 2 * e : e];
-        hi[g] = tp[a.tab.is64 ? 2 * e + 1 : e];
+      if constexpr (T64) {
+        lo[g] = trow[2 * e];
+        hi[g] = trow[2 * e + 1];
+      } else {
+        lo[g] = trow[e];
+        hi[g] = 0u;
       }
       sl[g] = 16 * grem;
       if (++grem == gpp) {
@@ -279,15 +287,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       }
     }
   };
-  if (PG == 2) load_ids(0, idlo, idhi, idin, slots);
-  const uint32_t kpage = PG == 2 ? (uint32_t)(a.tab.page * a.k.st) : 0u;
-  const uint32_t vpage = PG == 2 ? (uint32_t)(a.tab.page * a.v.st) : 0u;
+  if (G16) load_ids(0, idlo, idhi, idin, slots);
+  const uint32_t kpage = G16 ? (uint32_t)(a.tab.page * a.k.st) : 0u;
+  const uint32_t vpage = G16 ? (uint32_t)(a.tab.page * a.v.st) : 0u;
   const char* kbase = a.k.base + kvh * a.k.sh;
   const char* vbase = a.v.base + kvh * a.v.sh;
+  const uint64_t ksb = (uint32_t)a.k.sb, vsb = (uint32_t)a.v.sb;
+  const uint32_t nblk = (uint32_t)(a.tab.num_blocks < 0x7fffffff ? a.tab.num_blocks : 0x7fffffff);
   auto load_tile = [&](int t, uint4* kd, uint4* vd) {
     __amdgpu_buffer_rsrc_t rkg[NG], rvg[NG];
     uint32_t r0[NG];
-    if (PG == 2) {
+    if (G16) {
       uint32_t nlo[NG], nhi[NG], nsl[NG];
       bool nin[NG];
       load_ids(t + 1, nlo, nhi, nin, nsl);
@@ -295,13 +305,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       for (int g = 0; g < NG; ++g) {
         // valid: inside the range, high word zero (int64) or non-negative (int32), below num_blocks
         const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)idlo[g]);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)idhi[g]);
-        const bool valid = idin[g] && (a.tab.is64 ? hi == 0u : true) && (int64_t)lo < a.tab.num_blocks &&
-                           (a.tab.is64 || (int32_t)lo >= 0);
-        const int64_t bb = valid ? (int64_t)lo : 0;
+        const uint32_t hi = T64 ? (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)idhi[g]) : 0u;
+        // (an int32 id below nblk is non-negative: negative ids compare above it unsigned)
+        const bool valid = idin[g] && hi == 0u && lo < nblk;
+        const uint64_t bb = valid ? lo : 0u;
         r0[g] = slots[g];
-        rkg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * a.k.sb), 0, valid ? kpage : 0u, 0x00020000);
-        rvg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * a.v.sb), 0, valid ? vpage : 0u, 0x00020000);
+        // (block strides below 2^32, checked by the launcher: 32 x 32-bit products)
+        rkg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * ksb), 0, valid ? kpage : 0u, 0x00020000);
+        rvg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * vsb), 0, valid ? vpage : 0u, 0x00020000);
         idlo[g] = nlo[g];
         idhi[g] = nhi[g];
         idin[g] = nin[g];
@@ -312,7 +323,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     for (int i = 0; i < NLD; ++i) {
       const int c = tid + 256 * i, row = c / CH, ch = c % CH;
       const int64_t j = (int64_t)t * BN + row;
-      if (PG == 2) {
+      if (G16) {
         // the row's 16-row group: i * rows-per-pass / 16 when a pass covers at
         // most 16 rows (a constant), else plus the wave's part (uniform)
         constexpr int RPI = 256 / CH;
@@ -333,8 +344,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           }
         }
         const uint32_t slot = rx + (uint32_t)(row & 15);
-        const uint32_t ko = j < kend ? slot * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
-        const uint32_t vo = j < kend ? slot * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
+        const bool jin = (uint32_t)t * BN + (uint32_t)row < kend32;
+        const uint32_t ko = jin ? slot * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
+        const uint32_t vo = jin ? slot * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
         kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rkx, ko, 0, 0));
         vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvx, vo, 0, 0));
         continue;
@@ -841,9 +853,14 @@ hipError_t launch_prefill_t(const AttnArgs& a, int64_t nseq, int64_t max_len, hi
   const dim3 grid((unsigned)(tiles * (a.Hq / a.gh)));
   if (!PAGED)
     hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 0>), grid, dim3(256), 0, st, a);
-  else if (a.tab.page % 16 == 0)
-    hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 2>), grid, dim3(256), 0, st, a);
-  else
+  else if (a.tab.page % 16 == 0 && a.k.sb < (int64_t(1) << 32) && a.v.sb < (int64_t(1) << 32) && a.tab.cols > 0 &&
+           a.tab.cols * a.tab.page < (int64_t(1) << 31) && a.tab.num_blocks < (int64_t(1) << 31)) {
+    // whole 16-row groups per page, 32-bit table arithmetic
+    if (a.tab.is64)
+      hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 3>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 2>), grid, dim3(256), 0, st, a);
+  } else
     hipLaunchKernelGGL((attn_prefill_kernel<T, D, BN, 1>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
