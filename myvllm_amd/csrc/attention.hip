@@ -619,10 +619,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
   // block id of tile t's page (PAGE16), -1 past the range or for an entry
   // outside [0, num_blocks)
+  // (PAGE16: the sequence's table row is found once; a tile is 16-key group
+  // g0 + t of the split, in page g / gpp at slot 16 (g % gpp); key positions,
+  // table columns and block-offset products fit 32 bits, which the launcher
+  // checks, so no 64-bit division or product is left per tile)
+  const void* trow = PAGE16 ? reinterpret_cast<const char*>(a.tab.table) +
+                                  (a.tab.is64 ? 8 : 4) * (b * a.tab.row_stride)
+                            : nullptr;
+  const uint32_t gpp = PAGE16 ? (uint32_t)a.tab.page / 16u : 1u;
+  const uint32_t g0 = (uint32_t)k_lo / 16u;  // (chunk is a multiple of 16)
   auto tile_block = [&](int t) -> int64_t {
     if (!PAGE16 || t >= ntiles) return -1;
-    const int64_t col = (k_lo + 16 * (int64_t)t) / a.tab.page;
-    const int64_t blk = load_index_scalar(a.tab.table, b * a.tab.row_stride + col, a.tab.is64);
+    const uint32_t g = g0 + (uint32_t)t;
+    const uint32_t col = gpp == 1u ? g : g / gpp;
+    const int64_t blk = load_index_scalar(trow, col, a.tab.is64);
     return blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
   };
   // row r of tile t
@@ -635,20 +645,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
     return kv_row<true>(src, a.tab, b, 0, j, kvh);
   };
+  const char* kvk = a.k.base + kvh * a.k.sh;
+  const char* kvv = a.v.base + kvh * a.v.sh;
+  const uint64_t ksb = (uint32_t)a.k.sb, vsb = (uint32_t)a.v.sb;
   auto load_tile = [&](int t, int64_t blk, uint4* kd, uint4* vd) {
     if (PAGE16) {
       // one page per tile: buffer loads through a descriptor of this kv
       // head's rows of the page (32-bit offsets, rows past the range read 0)
-      const int64_t j0 = k_lo + 16 * (int64_t)t;
-      const int64_t nv = t < ntiles ? k_hi - j0 : 0;
+      const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;
+      const int32_t nv = t < ntiles ? (int32_t)((uint32_t)k_hi - j0) : 0;
       const uint32_t nvalid = blk < 0 ? 0u : (uint32_t)(nv < 16 ? nv : 16);
-      const uint32_t r0 = (uint32_t)(j0 % a.tab.page);
-      const int64_t bb = blk < 0 ? 0 : blk;
+      const uint32_t g = g0 + (uint32_t)t;
+      const uint32_t r0 = gpp == 1u ? 0u : 16u * (g - (g / gpp) * gpp);
+      const uint64_t bb = blk < 0 ? 0u : (uint32_t)blk;
       const uint32_t bytes = blk < 0 ? 0u : (uint32_t)(a.tab.page * a.k.st);
       const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(a.k.base + bb * a.k.sb + kvh * a.k.sh), 0, bytes, 0x00020000);
+          __builtin_amdgcn_make_buffer_rsrc((void*)(kvk + bb * ksb), 0, bytes, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(a.v.base + bb * a.v.sb + kvh * a.v.sh), 0, bytes, 0x00020000);
+          __builtin_amdgcn_make_buffer_rsrc((void*)(kvv + bb * vsb), 0, bytes, 0x00020000);
       const uint32_t kr = (uint32_t)(lane & 15);
       const uint32_t ko = kr < nvalid ? (r0 + kr) * (uint32_t)a.k.st + 16u * grp : 0x80000000u;
 #pragma unroll
@@ -703,10 +717,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   // second half: softmax of the scores (lane holds head column lane % 16,
   // keys 4 grp + r of the tile) and O^T += V^T P^T
   auto accumulate = [&](int t, f32x4 s) {
-    const int64_t j0 = k_lo + 16 * (int64_t)t;
+    const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;  // (key positions fit 32 bits)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      if (j0 + 4 * grp + r >= k_hi) s[r] = -INFINITY;
+      if (j0 + 4u * grp + r >= (uint32_t)k_hi) s[r] = -INFINITY;
     float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -884,7 +898,8 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t st) {
   const int hgroups = (a.Hq / a.Hkv + 15) / 16;
   const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv / a.kvw * hgroups), (unsigned)a.B);
   const size_t lds = (size_t)a.kvw * decode_lds_per_wave<T, D>();
-  if (a.tab.page % 16 == 0)
+  if (a.tab.page % 16 == 0 && a.k.sb < (int64_t(1) << 32) && a.v.sb < (int64_t(1) << 32) &&
+      a.tab.cols * a.tab.page < (int64_t(1) << 31) && a.tab.num_blocks < (int64_t(1) << 31))
     hipLaunchKernelGGL((attn_decode_kernel<T, D, true>), grid, dim3(64 * a.kvw), lds, st, a);
   else
     hipLaunchKernelGGL((attn_decode_kernel<T, D, false>), grid, dim3(64 * a.kvw), lds, st, a);
