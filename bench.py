@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_025_839_424,
-    "gdn_chunk_prefill_kernel/short": 3_851_921_920,
-    "gdn_recurrent_step_kernel": 1_083_302_704,
-    "causal_conv1d_varlen_kernel": 666_028_800,
-    "causal_conv1d_step_kernel": 59_316_832,
-    "gdn_decode_fused_kernel": 1_131_380_288,
-    "attn_prefill_kernel": 938_025_712,
-    "attn_decode_kernel": 1_268_935_544,  # with its combine kernel
-    "attn_paged_prefill_kernel": 821_463_360,
+    "gdn_chunk_prefill_kernel": 1_027_299_136,
+    "gdn_chunk_prefill_kernel/short": 3_848_439_264,
+    "gdn_recurrent_step_kernel": 1_083_423_200,
+    "causal_conv1d_varlen_kernel": 666_026_464,
+    "causal_conv1d_step_kernel": 59_316_416,
+    "gdn_decode_fused_kernel": 1_131_440_448,
+    "attn_prefill_kernel": 931_886_656,
+    "attn_decode_kernel": 1_268_981_288,  # with its combine kernel
+    "attn_paged_prefill_kernel": 820_016_160,
 }
 
 
@@ -819,7 +819,8 @@ def measure_peaks(dev, steps, warmup):
     torch_ms = _time_gpu(lambda _: dst.copy_(src), steps, warmup).median_ms
     return {"gemm_bf16_TFLOP_per_s": gemm, "gemm": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt)",
             "stream_GB_per_s": stream["GB_per_s"],
-            "stream": f"hbm_stream_copy_kernel, 1 GiB, {stream['blocks']} workgroups (read + write counted)",
+            "stream": "hbm_stream_copy_kernel, 1 GiB, " + (f"{stream['blocks']} workgroups" if stream["blocks"] else
+                                                           "one pass of 262,144 workgroups") + " (read + write counted)",
             "torch_copy_GB_per_s": 2 * (1 << 30) / (torch_ms * 1e-3) / 1e9}
 
 
