@@ -60,6 +60,22 @@ template <typename V4> GDN_DEVICE V4 tr4(const void* p) {
 
 GDN_DEVICE float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(x[l], x[l ^ 32]) in every lane l: one v_permlane32_swap of x with
+// itself (lanes 0..31 of one copy trade places with lanes 32..63 of the
+// other, so each lane then holds both of the pair's values), no LDS round
+// trip as a ds_bpermute would take.  (The two results are copied to scalars
+// before they are reinterpreted: this clang reads the first element of the
+// vector for __builtin_bit_cast(float, sw[1]).)  The maximum is a select:
+// fmaxf would first quiet both operands, two more instructions on the
+// softmax's dependency chain (the scores are never NaN).
+GDN_DEVICE float max_lane_pair32(float x) {
+  const uint32_t v = __builtin_bit_cast(uint32_t, x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const uint32_t ua = sw[0], ub = sw[1];
+  const float a = __builtin_bit_cast(float, ua), b = __builtin_bit_cast(float, ub);
+  return a > b ? a : b;
+}
+
 GDN_DEVICE int64_t clamp64(int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); }
 
 // An index at a wave-uniform position read through the scalar data cache (a
@@ -160,7 +176,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   constexpr bool QL = D == 256;
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // (the wave index through readfirstlane: the compiler then knows it, and
+  // the wave's query block, causal range and tile tests, to be uniform, so
+  // they live in scalar registers and branch without exec masks)
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = a.Hq / a.Hkv, gh = a.gh, qsubs = 4 / gh, groups = R / gh;
   // Workgroup order: sequence after sequence, a sequence's query tiles last
   // first, the head groups of a tile innermost.  The dispatcher deals
@@ -353,8 +372,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       }
       if (!PAGED) {
         // offsets past the descriptor's range (>= 2^31 > kend * stride) read zero
-        const uint32_t ko = j < kend ? (uint32_t)j * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
-        const uint32_t vo = j < kend ? (uint32_t)j * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
+        // (kend * stride fits 32 bits: the descriptor's range)
+        const uint32_t j32 = (uint32_t)t * BN + (uint32_t)row;
+        const uint32_t ko = j32 < kend32 ? j32 * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
+        const uint32_t vo = j32 < kend32 ? j32 * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
         kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
         vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
         continue;
@@ -378,7 +399,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 #pragma unroll
   for (int d = 0; d < NDT; ++d) oacc[d] = f32x16{};
   float m_used = -INFINITY, lsum = 0.f;
+  float nb = 0.f;  // -m_used, or 0 while m_used is -inf (the exponent offset)
 
+  // a key tile needs the mask when it reaches past the keys (t BN + BN > Lk)
+  // or, causal, past the wave's first query (t BN + BN - 1 > off + q0):
+  // t BN > mthr, one 32-bit test per tile (key positions stay below 2^31)
+  const int mthr = (int)clamp64(a.causal ? (Lk - BN < off + q0 - BN + 1 ? Lk - BN : off + q0 - BN + 1) : Lk - BN, -1,
+                                0x7fffffff);
   auto compute = [&](int t, int buf) {
     if ((int64_t)t * BN < kend_w) {
       const T* K = ks[buf];
@@ -407,7 +434,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       }
       // mask keys past the sequence / context and, if causal, past the query
       const int64_t tk0 = (int64_t)t * BN;
-      if (tk0 + BN > Lk || (a.causal && tk0 + BN - 1 > off + q0)) {
+      if (t * BN > mthr) {
         const int64_t lim = (a.causal ? (off + qi + 1 < Lk ? off + qi + 1 : Lk) : Lk) - tk0;
         const int rel = (int)clamp64(lim, -1, BN);  // keys of the tile at or past rel are masked
 #pragma unroll
@@ -416,24 +443,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           for (int r = 0; r < 16; ++r)
             if (32 * aa + 8 * (r >> 2) + 4 * hh + (r & 3) >= rel) s[aa][r] = -INFINITY;
       }
-      // tile maximum of the scaled scores (c > 0); masked scores are -inf and
-      // give p = exp2(-inf) = 0 below
+      // tile maximum of the scaled scores (c > 0) over this lane's half of
+      // the query's keys; masked scores are -inf and give p = exp2(-inf) = 0
+      // below.  The lane pair (l, l ^ 32) shares one base: it moves only when
+      // some lane's half exceeds it by 2^8, and then to the maximum over the
+      // pair, so the pair's maximum is taken only on that rare path (the
+      // same decisions and bases as taking it every tile)
       float mx = -INFINITY;
 #pragma unroll
       for (int aa = 0; aa < NA; ++aa)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[aa][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mt = mx * c;
-      if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
-        const float mn = fmaxf(m_used, mt);
+      if (__builtin_amdgcn_ballot_w64(mx * c > m_used + 8.f) != 0) {
+        const float mn = fmaxf(m_used, max_lane_pair32(mx) * c);
         const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
 #pragma unroll
         for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
         lsum *= alpha;
         m_used = mn;
+        nb = mn == -INFINITY ? 0.f : -mn;
       }
-      const float nb = m_used == -INFINITY ? 0.f : -m_used;
 #pragma unroll
       for (int aa = 0; aa < NA; ++aa) {
 #pragma unroll
@@ -516,13 +545,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int cpos = lane & (CH - 1), rsub = lane / CH;  // 16-byte piece of a row, row within the pass
     constexpr int RPP = 64 / CH;                           // rows per pass
+    const int qrem = (int)clamp64(len - q0, 0, 32);  // rows of this wave inside the sequence
+    T* const orow = reinterpret_cast<T*>(a.o) + (s0 + q0) * a.o_st + (int64_t)head * a.o_sh + 8 * cpos;
 #pragma unroll
     for (int r0 = 0; r0 < 32; r0 += RPP) {
       const int r = r0 + rsub;
       const v8 ov = *reinterpret_cast<const v8*>(qw + r * LDK + 8 * cpos);
-      if (q0 + r < len)
-        *reinterpret_cast<v8*>(reinterpret_cast<T*>(a.o) + (s0 + q0 + r) * a.o_st + (int64_t)head * a.o_sh +
-                               8 * cpos) = ov;
+      if (r < qrem) *reinterpret_cast<v8*>(orow + (int64_t)r * a.o_st) = ov;
     }
   } else if (qvalid) {
     T* op = reinterpret_cast<T*>(a.o) + (s0 + qi) * a.o_st + (int64_t)head * a.o_sh + 4 * hh;
@@ -694,6 +723,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
   for (int d = 0; d < NDT; ++d) oacc[d] = f32x4{};
   float m_used = -INFINITY, lsum = 0.f;
+  float nb = 0.f;  // -m_used, or 0 while m_used is -inf (the exponent offset)
   const float c = a.c > 0.f ? a.c : (a.c < 0.f ? -a.c : 1.f);
 
   // first half of a tile: its V rows to LDS (the previous tile's transposed
@@ -721,19 +751,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (j0 + 4u * grp + r >= (uint32_t)k_hi) s[r] = -INFINITY;
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mt = mx * c;  // c > 0; masked scores are -inf and give p = 0
-    if (__builtin_amdgcn_ballot_w64(mt > m_used + 8.f) != 0) {
-      const float mn = fmaxf(m_used, mt);
+    // maximum of this lane's 4 keys (c > 0; masked scores are -inf and give
+    // p = 0).  A head's 16 keys of the tile lie in the four 16-lane groups,
+    // which share one base: it moves only when some lane's keys exceed it by
+    // 2^8, and then to the maximum over the four lanes, taken only on that
+    // rare path (the same decisions and bases as taking it every tile)
+    const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    if (__builtin_amdgcn_ballot_w64(mx * c > m_used + 8.f) != 0) {
+      float mg = fmaxf(mx, __shfl_xor(mx, 16));
+      mg = fmaxf(mg, __shfl_xor(mg, 32));
+      const float mn = fmaxf(m_used, mg * c);
       const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
 #pragma unroll
       for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
       lsum *= alpha;
       m_used = mn;
+      nb = mn == -INFINITY ? 0.f : -mn;
     }
-    const float nb = m_used == -INFINITY ? 0.f : -m_used;
     v4 pf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

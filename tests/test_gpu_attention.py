@@ -61,6 +61,20 @@ def test_varlen_prefill_int64_cu_and_explicit_max(dev):
     assert_attn_close(out, flash_attention_prefill_ref(case.q, case.k, case.v, case.cu, case.scale))
 
 
+@pytest.mark.parametrize("Dh, causal", [(256, True), (256, False), (128, True), (64, True)])
+def test_varlen_prefill_sharp_scores(dev, Dh, causal):
+    """Scores spread over hundreds of exp2 units (scale 4 on unit-variance q, k):
+    the running maximum must be the maximum over both lane halves of a query's
+    keys, or the exponentials of the other half overflow to inf."""
+    case = attn_varlen_case([1, 33, 130], seed=Dh + causal, Hq=4, Hkv=2, D=Dh)
+    case.scale = 4.0
+    print(f"varlen sharp scores D={Dh} causal={causal}", flush=True)
+    out = _varlen(case, dev, causal)
+    ref = flash_attention_prefill_ref(case.q, case.k, case.v, case.cu, case.scale, is_causal=causal)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out, ref)
+
+
 def test_varlen_prefill_negative_scale(dev):
     case = attn_varlen_case([50, 7], seed=6, Hq=4, Hkv=2, D=64)
     case.scale = -0.2
