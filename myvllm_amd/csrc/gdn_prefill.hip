@@ -1238,7 +1238,7 @@ GDN_DEVICE void multi_run(const PrefillArgs& a, int64_t bid, int64_t nwg, int la
 template <bool F16, bool MULTI, bool PAD, bool OUT32>
 GDN_DEVICE void run_items(Smem& sm, const PrefillArgs& a, const Items& it, int tid) {
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: role branches and per-wave offsets in scalar registers)
   // padding sequences: zero output rows, no state (GDN_PREFILL_ACCUM_OUT: nothing to add)
   constexpr int kVec = OUT32 ? 4 : 8;  // output elements per 16-byte vector
   constexpr int kLanesPerRow = VD / kVec;
