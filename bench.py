@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_027_299_136,
-    "gdn_chunk_prefill_kernel/short": 3_848_439_264,
-    "gdn_recurrent_step_kernel": 1_083_423_200,
-    "causal_conv1d_varlen_kernel": 666_026_464,
-    "causal_conv1d_step_kernel": 59_316_416,
-    "gdn_decode_fused_kernel": 1_131_440_448,
-    "attn_prefill_kernel": 931_886_656,
-    "attn_decode_kernel": 1_268_981_288,  # with its combine kernel
-    "attn_paged_prefill_kernel": 820_016_160,
+    "gdn_chunk_prefill_kernel": 1_027_272_752,
+    "gdn_chunk_prefill_kernel/short": 3_860_927_520,
+    "gdn_recurrent_step_kernel": 1_083_325_888,
+    "causal_conv1d_varlen_kernel": 666_029_056,
+    "causal_conv1d_step_kernel": 59_318_272,
+    "gdn_decode_fused_kernel": 1_131_446_016,
+    "attn_prefill_kernel": 933_217_280,
+    "attn_decode_kernel": 1_269_113_912,  # with its combine kernel
+    "attn_paged_prefill_kernel": 821_886_656,
 }
 
 
