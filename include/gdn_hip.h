@@ -268,8 +268,10 @@ int gdn_gating(const gdn_tensor* a, const gdn_tensor* b, const gdn_tensor* A_log
  * flash_attention_varlen <- flash_attention_prefill, ops/full_attention.py:114-173
  *   q (T, Hq, D), k, v (T, Hkv, D), out (T, Hq, D), cu_seqlens (N+1,).
  *   Per sequence, query i attends keys 0..i (causal != 0) or all the
- *   sequence's keys.  max_seqlen must be at least the longest sequence
- *   (rows past it are left unwritten).
+ *   sequence's keys.  max_seqlen must be at least the longest sequence, as
+ *   the reference requires; here it only sizes the range check (the grid
+ *   covers every sequence's query tiles).  GDN_ERR_RANGE when
+ *   max(max_seqlen, 64) rows of k or v span 2^31 bytes or more.
  */
 int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, const gdn_tensor* v,
                            const gdn_tensor* cu_seqlens, gdn_tensor* out, int64_t max_seqlen, float scale,

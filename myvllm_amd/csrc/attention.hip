@@ -251,12 +251,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 
   // staging of a K/V tile: global rows -> registers (rows past kend read as
   // zero, so a tile past the range loads nothing) -> LDS
-  // packed rows: buffer loads through descriptors of this sequence's kv-head
-  // rows [0, kend) (32-bit offsets; rows past kend read as zero)
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.k.base + s0 * a.k.st + kvh * a.k.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.k.st), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.v.base + s0 * a.v.st + kvh * a.v.sh), 0, PAGED ? 0u : (uint32_t)(kend * a.v.st), 0x00020000);
+  // packed rows: per key tile, buffer descriptors of the tile's rows of this
+  // sequence's kv head whose range ends at the last row before kend (rows
+  // past it read as zero, 32-bit offsets): a lane's offsets are the same for
+  // every tile, and the tile's position and bound are scalar arithmetic
+  const char* const kseq = a.k.base + s0 * a.k.st + kvh * a.k.sh;
+  const char* const vseq = a.v.base + s0 * a.v.st + kvh * a.v.sh;
   constexpr int NG = BN / 16;  // 16-row groups of a tile
   static_assert(CH >= 8 && 64 % CH == 0, "a wave's rows of a tile lie in one 16-row group");
   // PG 2, 3: each 16-row group of a tile lies in one page.  Its block id is a
@@ -307,15 +307,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     }
   };
   if (G16) load_ids(0, idlo, idhi, idin, slots);
-  const uint32_t kpage = G16 ? (uint32_t)(a.tab.page * a.k.st) : 0u;
-  const uint32_t vpage = G16 ? (uint32_t)(a.tab.page * a.v.st) : 0u;
+  const uint32_t kst = (uint32_t)a.k.st, vst = (uint32_t)a.v.st;  // row strides in bytes (below 2^31)
   const char* kbase = a.k.base + kvh * a.k.sh;
   const char* vbase = a.v.base + kvh * a.v.sh;
   const uint64_t ksb = (uint32_t)a.k.sb, vsb = (uint32_t)a.v.sb;
   const uint32_t nblk = (uint32_t)(a.tab.num_blocks < 0x7fffffff ? a.tab.num_blocks : 0x7fffffff);
   auto load_tile = [&](int t, uint4* kd, uint4* vd) {
-    __amdgpu_buffer_rsrc_t rkg[NG], rvg[NG];
+    __amdgpu_buffer_rsrc_t rkg[NG], rvg[NG], rkt, rvt;
     uint32_t r0[NG];
+    if (!PAGED) {
+      const uint32_t t0 = (uint32_t)t * BN;
+      const uint32_t nv = t0 < kend32 ? (kend32 - t0 < (uint32_t)BN ? kend32 - t0 : (uint32_t)BN) : 0u;
+      rkt = __builtin_amdgcn_make_buffer_rsrc((void*)(kseq + (uint64_t)t0 * kst), 0, nv * kst, 0x00020000);
+      rvt = __builtin_amdgcn_make_buffer_rsrc((void*)(vseq + (uint64_t)t0 * vst), 0, nv * vst, 0x00020000);
+    }
     if (G16) {
       uint32_t nlo[NG], nhi[NG], nsl[NG];
       bool nin[NG];
@@ -329,9 +334,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
         const bool valid = idin[g] && hi == 0u && lo < nblk;
         const uint64_t bb = valid ? lo : 0u;
         r0[g] = slots[g];
+        // the group's rows before kend: its range ends after them in the page,
+        // so the rows past kend read as zero with no test per row
+        const uint32_t j0 = (uint32_t)t * BN + 16u * g;
+        const uint32_t ends = slots[g] + (j0 < kend32 ? (kend32 - j0 < 16u ? kend32 - j0 : 16u) : 0u);
         // (block strides below 2^32, checked by the launcher: 32 x 32-bit products)
-        rkg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * ksb), 0, valid ? kpage : 0u, 0x00020000);
-        rvg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * vsb), 0, valid ? vpage : 0u, 0x00020000);
+        rkg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * ksb), 0, valid ? ends * kst : 0u, 0x00020000);
+        rvg[g] = __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * vsb), 0, valid ? ends * vst : 0u, 0x00020000);
         idlo[g] = nlo[g];
         idhi[g] = nhi[g];
         idin[g] = nin[g];
@@ -363,21 +372,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           }
         }
         const uint32_t slot = rx + (uint32_t)(row & 15);
-        const bool jin = (uint32_t)t * BN + (uint32_t)row < kend32;
-        const uint32_t ko = jin ? slot * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
-        const uint32_t vo = jin ? slot * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
-        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rkx, ko, 0, 0));
-        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvx, vo, 0, 0));
+        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rkx, slot * kst + 16u * ch, 0, 0));
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvx, slot * vst + 16u * ch, 0, 0));
         continue;
       }
       if (!PAGED) {
-        // offsets past the descriptor's range (>= 2^31 > kend * stride) read zero
-        // (kend * stride fits 32 bits: the descriptor's range)
-        const uint32_t j32 = (uint32_t)t * BN + (uint32_t)row;
-        const uint32_t ko = j32 < kend32 ? j32 * (uint32_t)a.k.st + 16u * ch : 0x80000000u;
-        const uint32_t vo = j32 < kend32 ? j32 * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
-        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
-        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+        // (the row offset times the stride fits 32 bits: the launcher checks
+        // max(max_seqlen, 64) rows of either stride against 2^31)
+        kd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rkt, (uint32_t)row * kst + 16u * ch, 0, 0));
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvt, (uint32_t)row * vst + 16u * ch, 0, 0));
         continue;
       }
       const char* pk = j < kend ? kv_row<PAGED>(a.k, a.tab, n, s0, j, kvh) : nullptr;

@@ -461,9 +461,11 @@ GDN_EXPORT int flash_attention_varlen(const gdn_tensor* q, const gdn_tensor* k, 
   const int64_t gh = R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1);
   if (cu_seqlens->shape[0] - 1 > kMaxGridYZ || q->shape[1] / gh > kMaxGridYZ || max_seqlen / 32 > kMaxGrid)
     return GDN_ERR_RANGE;
-  // a sequence's kv rows are addressed with 32-bit byte offsets below 2^31
+  // a sequence's kv rows, and a 64-row key tile of them, are addressed with
+  // 32-bit byte offsets below 2^31
   const int64_t es = elem_size(k->dtype);
-  if (max_seqlen * std::max(k->stride[0], v->stride[0]) * es >= (int64_t(1) << 31)) return GDN_ERR_RANGE;
+  if (std::max<int64_t>(max_seqlen, 64) * std::max(k->stride[0], v->stride[0]) * es >= (int64_t(1) << 31))
+    return GDN_ERR_RANGE;
   return launch_rc(attn_varlen_prefill_launch(q, k, v, cu_seqlens, out, max_seqlen, scale, causal,
                                               reinterpret_cast<hipStream_t>(stream)));
 }

@@ -320,6 +320,18 @@ def test_varlen_attention_validation(mutate, code):
     assert _call_varlen_attn(a) == ERR[code]
 
 
+@cpu_only
+@pytest.mark.parametrize("max_len, code", [(5, "RANGE"), (2**20, "RANGE")])
+def test_varlen_attention_key_tile_range(max_len, code):
+    """A 64-row key tile of k or v must span less than 2^31 bytes whatever
+    max_seqlen says (2^24-element rows: 5 rows fit, 64 do not)."""
+    a = _varlen_attn_args()
+    k = D(a["k"])
+    k.stride[0] = 2**24
+    rc = _lib.load().flash_attention_varlen(D(a["q"]), k, D(a["v"]), D(a["cu"]), D(a["out"]), max_len, 1.0, 1, None)
+    assert rc == ERR[code]
+
+
 def _paged_attn_args(B=2, Hq=4, Hkv=2, Dh=128, blocks=5, page=16, cols=3, dtype=torch.bfloat16):
     return dict(q=torch.zeros(B, Hq, Dh, dtype=dtype), kc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype),
                 vc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype), tab=torch.zeros(B, cols, dtype=torch.int32),
