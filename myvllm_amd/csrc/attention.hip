@@ -690,21 +690,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       const uint32_t g = g0 + (uint32_t)t;
       const uint32_t r0 = gpp == 1u ? 0u : 16u * (g - (g / gpp) * gpp);
       const uint64_t bb = blk < 0 ? 0u : (uint32_t)blk;
-      const uint32_t bytes = blk < 0 ? 0u : (uint32_t)(a.tab.page * a.k.st);
+      // the ranges end after the tile's valid rows in the page, so the rows
+      // past them read as zero with no test per row
+      const uint32_t kst = (uint32_t)a.k.st, vst = (uint32_t)a.v.st;
       const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(kvk + bb * ksb), 0, bytes, 0x00020000);
+          __builtin_amdgcn_make_buffer_rsrc((void*)(kvk + bb * ksb), 0, (r0 + nvalid) * kst, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(kvv + bb * vsb), 0, bytes, 0x00020000);
-      const uint32_t kr = (uint32_t)(lane & 15);
-      const uint32_t ko = kr < nvalid ? (r0 + kr) * (uint32_t)a.k.st + 16u * grp : 0x80000000u;
+          __builtin_amdgcn_make_buffer_rsrc((void*)(kvv + bb * vsb), 0, (r0 + nvalid) * vst, 0x00020000);
+      const uint32_t ko = (r0 + (uint32_t)(lane & 15)) * kst + 16u * grp;
 #pragma unroll
       for (int s = 0; s < NKS; ++s)
         kd[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64u * s, 0, 0));
 #pragma unroll
       for (int i = 0; i < NLD; ++i) {
         const uint32_t cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-        const uint32_t vo = row < nvalid ? (r0 + row) * (uint32_t)a.v.st + 16u * ch : 0x80000000u;
-        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, (r0 + row) * vst + 16u * ch, 0, 0));
       }
       return;
     }
