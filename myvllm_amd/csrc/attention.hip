@@ -174,6 +174,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   // the allocator kept one fragment buffer, so every LDS read was waited for
   // right before its MFMA)
   constexpr bool QL = D == 256;
+  // of those, the last QRG stay in registers as well (fewer LDS reads in the
+  // score phase for 32 or 48 more registers; measured: 8 packed, 12 paged,
+  // all 16 much slower)
+  constexpr int QRG = QL ? (PG == 0 ? 8 : 12) : 0;
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   // (the wave index through readfirstlane: the compiler then knows it, and
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     }
     if constexpr (QL) {
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) *reinterpret_cast<v8*>(qw + col * LDK + 16 * s + 8 * hh) = qf[s];
+      for (int s = 0; s < NKS - QRG; ++s) *reinterpret_cast<v8*>(qw + col * LDK + 16 * s + 8 * hh) = qf[s];
     }
   };
 
@@ -422,13 +426,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           const T* qp = qw + col * LDK + 8 * hh;
 #pragma unroll
           for (int k = 0; k < NKS; ++k)
-            s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), *reinterpret_cast<const v8*>(qp + 16 * k), s[aa]);
+            s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k),
+                           k >= NKS - QRG ? qf[k] : *reinterpret_cast<const v8*>(qp + 16 * k), s[aa]);
           // schedule: the K and Q fragments of the next k-steps are read while each MFMA runs
           __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
 #pragma unroll
           for (int k = 0; k < NKS; ++k) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            if (k + 2 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            if (k + 2 < NKS - QRG) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            else if (k + 2 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           }
         } else {
 #pragma unroll
