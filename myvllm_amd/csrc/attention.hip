@@ -413,7 +413,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   // t BN > mthr, one 32-bit test per tile (key positions stay below 2^31)
   const int mthr = (int)clamp64(a.causal ? (Lk - BN < off + q0 - BN + 1 ? Lk - BN : off + q0 - BN + 1) : Lk - BN, -1,
                                 0x7fffffff);
-  auto compute = [&](int t, int buf) {
+  // `mid` (the next tiles' LDS stores and global loads) is issued right after
+  // the score MFMAs, so that its issue overlaps their execution; a wave with
+  // no keys left in this tile still runs it
+  auto compute = [&](int t, int buf, auto&& mid) {
     if ((int64_t)t * BN < kend_w) {
       const T* K = ks[buf];
       const T* V = vs[buf];
@@ -441,6 +444,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           for (int k = 0; k < NKS; ++k) s[aa] = M::m32(*reinterpret_cast<const v8*>(kp + 16 * k), qf[k], s[aa]);
         }
       }
+      mid();
       // mask keys past the sequence / context and, if causal, past the query
       const int64_t tk0 = (int64_t)t * BN;
       if (t * BN > mthr) {
@@ -510,6 +514,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
           }
         }
       }
+    } else {
+      mid();
     }
   };
 
@@ -522,15 +528,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   load_tile(1, kB, vB);
   load_tile(2, kA, vA);
   __syncthreads();
+  // (packed rows: the next tiles' stores and loads go out between the score
+  // MFMAs and the softmax; paged rows: after the tile, since their loads
+  // first wait for the block ids, and the longer live ranges cost registers)
   for (int t = 0; t < ntiles; t += 2) {
-    compute(t, 0);
-    store_tile(1, kB, vB);
-    load_tile(t + 3, kB, vB);
-    __syncthreads();
-    compute(t + 1, 1);
-    store_tile(0, kA, vA);
-    load_tile(t + 4, kA, vA);
-    __syncthreads();
+    if constexpr (PG == 0) {
+      compute(t, 0, [&]() __attribute__((always_inline)) {
+        store_tile(1, kB, vB);
+        load_tile(t + 3, kB, vB);
+      });
+      __syncthreads();
+      compute(t + 1, 1, [&]() __attribute__((always_inline)) {
+        store_tile(0, kA, vA);
+        load_tile(t + 4, kA, vA);
+      });
+      __syncthreads();
+    } else {
+      const auto after = []() {};  // (one instantiation of compute for both calls)
+      compute(t, 0, after);
+      store_tile(1, kB, vB);
+      load_tile(t + 3, kB, vB);
+      __syncthreads();
+      compute(t + 1, 1, after);
+      store_tile(0, kA, vA);
+      load_tile(t + 4, kA, vA);
+      __syncthreads();
+    }
   }
 
   const float lt = lsum + __shfl_xor(lsum, 32);
