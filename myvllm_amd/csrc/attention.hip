@@ -175,9 +175,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
   // right before its MFMA)
   constexpr bool QL = D == 256;
   // of those, the last QRG stay in registers as well (fewer LDS reads in the
-  // score phase for 32 or 48 more registers; measured: 8 packed, 12 paged,
-  // all 16 much slower)
-  constexpr int QRG = QL ? (PG == 0 ? 8 : 12) : 0;
+  // score phase for 48 more registers; measured: 12 of 16, all 16 much slower)
+  constexpr int QRG = QL ? 12 : 0;
   __shared__ __align__(16) T qs[QL ? 4 * 32 * LDK : 8];
 
   // (the wave index through readfirstlane: the compiler then knows it, and
