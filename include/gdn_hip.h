@@ -297,10 +297,11 @@ int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_cache, cons
 /*
  * paged_attention_decode <- paged_flash_attention_decode, ops/full_attention.py:282-335
  *   q, out (B, Hq, D): one query per sequence, at position context_lens[b] - 1;
- *   caches and block_tables (B, max_blocks) as above.  Split s (of num_splits,
- *   1..256) covers keys [s c, (s+1) c) with c = max_blocks * page / num_splits
- *   rounded up to 16; the splits that hold keys are merged by a second
- *   launch.  With num_splits > 1, workspace is an fp32 1-D tensor of at least
+ *   caches and block_tables (B, max_blocks) as above.  With c = max_blocks *
+ *   page / num_splits (num_splits 1..256) rounded up to 16, sequence b uses
+ *   n_b = clamp(ceil(L_b / c), 1, num_splits) splits and its 16-key tiles are
+ *   dealt evenly over them (split s holds tiles [s T_b / n_b, (s+1) T_b / n_b),
+ *   T_b = ceil(L_b / 16)); the splits are merged by a second launch.  With num_splits > 1, workspace is an fp32 1-D tensor of at least
  *   paged_attention_decode_workspace_size(B, Hq, D, num_splits) elements
  *   (16-byte aligned), overwritten.  context_lens[b] = 0 gives a zero row.
  */

@@ -652,9 +652,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int64_t b = blockIdx.z;
   const int64_t ctx = load_index(a.ctx, b, a.ctx64);
   const int64_t L = clamp64(ctx, 0, a.tab.cols * a.tab.page);
-  const int64_t k_lo = a.chunk * split;
-  if (split > 0 && k_lo >= L) return;  // no keys: the combine skips this split
-  const int64_t k_hi = k_lo + a.chunk < L ? k_lo + a.chunk : L;
+  // the sequence uses nsplit = ceil(L / chunk) of the splits (at least one,
+  // at most num_splits; the combine counts them the same way), and its
+  // 16-key tiles are dealt evenly over them: no split of a sequence holds
+  // more than one tile above another's, so no short tail split leaves its
+  // siblings' CUs the work
+  const int64_t nsp = (L + a.chunk - 1) / a.chunk;
+  const int nsplit = (int)(nsp < 1 ? 1 : (nsp > a.splits ? a.splits : nsp));
+  if (split >= nsplit) return;  // no keys: the combine skips this split
+  const int64_t tiles_all = (L + 15) / 16;
+  const int64_t k_lo = 16 * (tiles_all * split / nsplit);
+  const int64_t k_hi_t = 16 * (tiles_all * (split + 1) / nsplit);
+  const int64_t k_hi = k_hi_t < L ? k_hi_t : L;
   const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
 
   const int R = a.Hq / a.Hkv, hgroups = (R + 15) / 16;
@@ -687,7 +696,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
                                   (a.tab.is64 ? 8 : 4) * (b * a.tab.row_stride)
                             : nullptr;
   const uint32_t gpp = PAGE16 ? (uint32_t)a.tab.page / 16u : 1u;
-  const uint32_t g0 = (uint32_t)k_lo / 16u;  // (chunk is a multiple of 16)
+  const uint32_t g0 = (uint32_t)k_lo / 16u;  // (k_lo is a multiple of 16)
   auto tile_block = [&](int t) -> int64_t {
     if (!PAGE16 || t >= ntiles) return -1;
     const uint32_t g = g0 + (uint32_t)t;
