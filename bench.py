@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_027_300_048,
-    "gdn_chunk_prefill_kernel/short": 3_869_907_296,
-    "gdn_recurrent_step_kernel": 1_083_291_712,
-    "causal_conv1d_varlen_kernel": 666_028_256,
-    "causal_conv1d_step_kernel": 59_314_816,
-    "gdn_decode_fused_kernel": 1_131_392_640,
-    "attn_prefill_kernel": 933_050_912,
-    "attn_decode_kernel": 1_269_112_104,  # with its combine kernel
-    "attn_paged_prefill_kernel": 821_777_376,
+    "gdn_chunk_prefill_kernel": 1_027_065_248,
+    "gdn_chunk_prefill_kernel/short": 3_853_873_696,
+    "gdn_recurrent_step_kernel": 1_083_326_880,
+    "causal_conv1d_varlen_kernel": 666_040_192,
+    "causal_conv1d_step_kernel": 59_315_168,
+    "gdn_decode_fused_kernel": 1_131_470_752,
+    "attn_prefill_kernel": 933_014_528,
+    "attn_decode_kernel": 1_269_160_960,  # with its combine kernel
+    "attn_paged_prefill_kernel": 821_919_872,
 }
 
 
