@@ -297,13 +297,20 @@ int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_cache, cons
 /*
  * paged_attention_decode <- paged_flash_attention_decode, ops/full_attention.py:282-335
  *   q, out (B, Hq, D): one query per sequence, at position context_lens[b] - 1;
- *   caches and block_tables (B, max_blocks) as above.  With c = max_blocks *
- *   page / num_splits (num_splits 1..256) rounded up to 16, sequence b uses
- *   n_b = clamp(ceil(L_b / c), 1, num_splits) splits and its 16-key tiles are
- *   dealt evenly over them (split s holds tiles [s T_b / n_b, (s+1) T_b / n_b),
- *   T_b = ceil(L_b / 16)); the splits are merged by a second launch.  With num_splits > 1, workspace is an fp32 1-D tensor of at least
+ *   caches and block_tables (B, max_blocks) as above.  num_splits 1..256.
+ *   One split: a wave per (sequence, kv head) streams the whole sequence.
+ *   num_splits > 1: the batch is dealt over U = B * (num_splits - 1) units of
+ *   equal price, sequence b costing ceil(L_b / 16) 16-key tiles plus 2 (0
+ *   when L_b = 0), so every unit streams about the same number of keys
+ *   whatever the lengths; a unit may hold the end of one sequence and the
+ *   start of the next, and the pieces are merged by a second launch.  The
+ *   sequences' total price must stay below 2^31: B * (ceil(max_blocks * page
+ *   / 16) + 2) >= 2^31 returns GDN_ERR_RANGE.  With num_splits > 1,
+ *   workspace is an fp32 1-D tensor of at least
  *   paged_attention_decode_workspace_size(B, Hq, D, num_splits) elements
- *   (16-byte aligned), overwritten.  context_lens[b] = 0 gives a zero row.
+ *   (16-byte aligned), overwritten: B * num_splits * Hq * (D + 4) partials
+ *   (one slot per piece; a piece is a (sequence, unit) pair) and the B + 1
+ *   price prefix.  context_lens[b] = 0 gives a zero row.
  */
 int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim,
                                               int32_t num_splits);

@@ -599,20 +599,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Paged decode: one wave per (sequence, kv head, group of up to 16 query
-// heads, key split).  The query heads of one kv head are the 16 columns of
+// Paged decode: one wave per (kv head, group of up to 16 query heads) of a
+// work unit.  The query heads of one kv head are the 16 columns of
 // S^T = K Q^T (16x16x32 MFMA, K fragments straight from global memory), the
 // V tile goes through a wave-private LDS tile for the transposed read of
-// O^T = V^T P^T (16x16x16 MFMA).  Split s covers keys [s chunk, (s+1) chunk)
-// of the table's capacity (chunk fixed per launch), so the waves of all
-// sequences get equal work and splits past a sequence's length exit at once.
-// With more than one split the wave writes its unnormalised O, running
-// maximum and row sum to the workspace and attn_decode_combine_kernel merges
-// the splits that hold keys.  With a page size that is a multiple of 16 a
-// 16-key tile lies in one page: its block id is one wave-uniform load, issued
-// a tile ahead of the K/V loads that use it.  The kvw kv heads of a workgroup
-// (one wave each) read the interleaved head rows of the same cache slots at
-// about the same time, so each page is streamed as one contiguous region.
+// O^T = V^T P^T (16x16x16 MFMA).  With one split a unit is one sequence and
+// the wave writes the normalised output.  With num_splits > 1 the batch is
+// dealt evenly over U = B (num_splits - 1) units by price: sequence b costs
+// its 16-key tiles T_b = ceil(L_b / 16) plus kDecodeStartPrice for the start
+// of a piece (its query load and pipeline fill), 0 if it has no keys; laid
+// end to end the sequences fill prices [0, Q_B), sequence b's tiles at
+// [Q_b + kDecodeStartPrice, Q_{b+1}), and unit u takes the tiles whose prices
+// lie in [u Q_B / U, (u+1) Q_B / U).  So every unit streams about the same
+// number of keys whatever the lengths are.  A unit crossing sequence ends
+// runs one piece per sequence, and each piece (sequence b, unit u) writes its
+// unnormalised O, running maximum and row sum to workspace slot b + u < B +
+// U (distinct for distinct pieces: a later piece has a later unit or a later
+// sequence and neither index decreases), which attn_decode_combine_kernel
+// merges.  The price prefix Q is summed by the decode waves themselves for
+// batches of up to 1,024 sequences, else by attn_decode_prices_kernel,
+// launched first.  With a page size that is a multiple of 16 a 16-key tile
+// lies in one page: its block id is one wave-uniform load, issued a tile ahead
+// of the K/V loads that use it.  The kvw kv heads of a workgroup (one wave
+// each) read the interleaved head rows of the same cache slots at about the
+// same time, so each page is streamed as one contiguous region.
+constexpr int32_t kDecodeStartPrice = 2;
+
 struct DecodeArgs {
   const void* q;
   int64_t q_ss, q_sh;
@@ -621,12 +633,54 @@ struct DecodeArgs {
   int64_t o_ss, o_sh;
   const void* ctx;
   PagedTable tab;
-  float* part;  // (B, Hq, splits, D + 4): O, m, l (rows padded to 16 bytes)
-  int64_t chunk;  // keys per split, a multiple of 16
+  float* part;     // (B + U = B splits, Hq, D + 4): O, m, l per piece (rows padded to 16 bytes)
+  int32_t* prices;  // (B + 1): the price prefix Q (splits > 1)
   int32_t B, Hq, Hkv, splits, kvw;
+  int32_t units;  // splits > 1: units per sequence, splits - 1 (U = B units)
   float c;
   bool ctx64;
+  bool prices_inline;  // the decode waves compute Q themselves (small batches)
 };
+
+// Price prefix of the batch for the split decode: Q[b] = sum over b' < b of
+// the price of b' (ceil(L_b' / 16) + kDecodeStartPrice, or 0 with no keys),
+// Q[B] the total, with L_b the context length clamped to the table's capacity
+// as the decode clamps it.  One workgroup: each thread sums a contiguous run of
+// sequences, the run sums are scanned across the block, and each thread writes
+// its run's prefixes.  (Q[B] < 2^31: the entry point checks
+// B * (ceil(capacity / 16) + kDecodeStartPrice).)
+__global__ __launch_bounds__(1024) void attn_decode_prices_kernel(const DecodeArgs a) {
+  __shared__ int32_t wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t cap = a.tab.cols * a.tab.page;
+  const int per = (a.B + 1023) / 1024;
+  const int64_t b0 = (int64_t)tid * per;
+  auto tiles_of = [&](int64_t b) -> int32_t {
+    const int32_t t = b < a.B ? (int32_t)((clamp64(load_index(a.ctx, b, a.ctx64), 0, cap) + 15) / 16) : 0;
+    return t > 0 ? t + kDecodeStartPrice : 0;
+  };
+  int32_t sum = 0;
+  for (int i = 0; i < per; ++i) sum += tiles_of(b0 + i);
+  // inclusive scan over the wave, then over the 16 wave totals
+  int32_t inc = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d *= 2) {
+    const int32_t y = __shfl_up(inc, d);
+    if (lane >= d) inc += y;
+  }
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int32_t base = 0;
+  for (int i = 0; i < w; ++i) base += wsum[i];
+  int32_t run = base + inc - sum;  // exclusive prefix of this thread's run
+  for (int i = 0; i < per; ++i) {
+    const int64_t b = b0 + i;
+    if (b >= a.B) break;
+    a.prices[b] = run;
+    run += tiles_of(b);
+  }
+  if (tid == 1023) a.prices[a.B] = base + inc;
+}
 
 // LDS bytes of one decode wave: a 16-row V tile with a 32-byte row skew and
 // the wave's query fragments
@@ -648,23 +702,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   // this wave's LDS: the V tile, then its query fragments
   T* vs = reinterpret_cast<T*>(decode_smem + wv * decode_lds_per_wave<T, D>());
   v8* qs = reinterpret_cast<v8*>(vs + 16 * LDV);
-  const int split = blockIdx.x;
-  const int64_t b = blockIdx.z;
-  const int64_t ctx = load_index(a.ctx, b, a.ctx64);
-  const int64_t L = clamp64(ctx, 0, a.tab.cols * a.tab.page);
-  // the sequence uses nsplit = ceil(L / chunk) of the splits (at least one,
-  // at most num_splits; the combine counts them the same way), and its
-  // 16-key tiles are dealt evenly over them: no split of a sequence holds
-  // more than one tile above another's, so no short tail split leaves its
-  // siblings' CUs the work
-  const int64_t nsp = (L + a.chunk - 1) / a.chunk;
-  const int nsplit = (int)(nsp < 1 ? 1 : (nsp > a.splits ? a.splits : nsp));
-  if (split >= nsplit) return;  // no keys: the combine skips this split
-  const int64_t tiles_all = (L + 15) / 16;
-  const int64_t k_lo = 16 * (tiles_all * split / nsplit);
-  const int64_t k_hi_t = 16 * (tiles_all * (split + 1) / nsplit);
-  const int64_t k_hi = k_hi_t < L ? k_hi_t : L;
-  const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
+  const int64_t cap = a.tab.cols * a.tab.page;
 
   const int R = a.Hq / a.Hkv, hgroups = (R + 15) / 16;
   const int kvh = (blockIdx.y / hgroups) * a.kvw + wv;
@@ -672,227 +710,361 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const bool hvalid = hcol < R;
   const int head = kvh * R + (hvalid ? hcol : 0);
   const int grp = lane >> 4;
-
-  // query fragments (B operand of S^T): lane holds head column lane % 16,
-  // dims 32 s + 8 grp .. +7; kept in LDS to leave registers for two tiles in flight
-  {
-    const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_ss + (int64_t)head * a.q_sh + 8 * grp;
-    // a negative scale is folded into q (an exact sign flip), a zero scale is
-    // q = 0 with c = 1 (equal weights), so the softmax below has c > 0
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      const v8 qv = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
-      qs[s * 64 + lane] = a.c > 0.f ? qv : (a.c < 0.f ? -qv : v8{});
-    }
-  }
-
-  // block id of tile t's page (PAGE16), -1 past the range or for an entry
-  // outside [0, num_blocks)
-  // (PAGE16: the sequence's table row is found once; a tile is 16-key group
-  // g0 + t of the split, in page g / gpp at slot 16 (g % gpp); key positions,
-  // table columns and block-offset products fit 32 bits, which the launcher
-  // checks, so no 64-bit division or product is left per tile)
-  const void* trow = PAGE16 ? reinterpret_cast<const char*>(a.tab.table) +
-                                  (a.tab.is64 ? 8 : 4) * (b * a.tab.row_stride)
-                            : nullptr;
-  const uint32_t gpp = PAGE16 ? (uint32_t)a.tab.page / 16u : 1u;
-  const uint32_t g0 = (uint32_t)k_lo / 16u;  // (k_lo is a multiple of 16)
-  auto tile_block = [&](int t) -> int64_t {
-    if (!PAGE16 || t >= ntiles) return -1;
-    const uint32_t g = g0 + (uint32_t)t;
-    const uint32_t col = gpp == 1u ? g : g / gpp;
-    const int64_t blk = load_index_scalar(trow, col, a.tab.is64);
-    return blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
-  };
-  // row r of tile t
-  auto row_ptr = [&](const KvSource& src, int t, int64_t blk, int r) -> const char* {
-    const int64_t j = k_lo + 16 * (int64_t)t + r;
-    if (j >= k_hi) return nullptr;
-    if (PAGE16) {
-      if (blk < 0) return nullptr;
-      return src.base + blk * src.sb + (j % a.tab.page) * src.st + kvh * src.sh;
-    }
-    return kv_row<true>(src, a.tab, b, 0, j, kvh);
-  };
   const char* kvk = a.k.base + kvh * a.k.sh;
   const char* kvv = a.v.base + kvh * a.v.sh;
   const uint64_t ksb = (uint32_t)a.k.sb, vsb = (uint32_t)a.v.sb;
-  auto load_tile = [&](int t, int64_t blk, uint4* kd, uint4* vd) {
-    if (PAGE16) {
-      // one page per tile: buffer loads through a descriptor of this kv
-      // head's rows of the page (32-bit offsets, rows past the range read 0)
-      const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;
-      const int32_t nv = t < ntiles ? (int32_t)((uint32_t)k_hi - j0) : 0;
-      const uint32_t nvalid = blk < 0 ? 0u : (uint32_t)(nv < 16 ? nv : 16);
-      const uint32_t g = g0 + (uint32_t)t;
-      const uint32_t r0 = gpp == 1u ? 0u : 16u * (g - (g / gpp) * gpp);
-      const uint64_t bb = blk < 0 ? 0u : (uint32_t)blk;
-      // the ranges end after the tile's valid rows in the page, so the rows
-      // past them read as zero with no test per row
-      const uint32_t kst = (uint32_t)a.k.st, vst = (uint32_t)a.v.st;
-      const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(kvk + bb * ksb), 0, (r0 + nvalid) * kst, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(kvv + bb * vsb), 0, (r0 + nvalid) * vst, 0x00020000);
-      const uint32_t ko = (r0 + (uint32_t)(lane & 15)) * kst + 16u * grp;
-#pragma unroll
-      for (int s = 0; s < NKS; ++s)
-        kd[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64u * s, 0, 0));
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        const uint32_t cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-        vd[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, (r0 + row) * vst + 16u * ch, 0, 0));
-      }
-      return;
-    }
-    {
-      const char* pk = row_ptr(a.k, t, blk, lane & 15);
-#pragma unroll
-      for (int s = 0; s < NKS; ++s)
-        kd[s] = pk ? *reinterpret_cast<const uint4*>(pk + 2 * (32 * s + 8 * grp)) : uint4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-      const char* pv = row_ptr(a.v, t, blk, row);
-      vd[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
-    }
-  };
-
-  f32x4 oacc[NDT];
-#pragma unroll
-  for (int d = 0; d < NDT; ++d) oacc[d] = f32x4{};
-  float m_used = -INFINITY, lsum = 0.f;
-  float nb = 0.f;  // -m_used, or 0 while m_used is -inf (the exponent offset)
   const float c = a.c > 0.f ? a.c : (a.c < 0.f ? -a.c : 1.f);
 
-  // first half of a tile: its V rows to LDS (the previous tile's transposed
-  // reads were issued earlier by this wave, and LDS operations of a wave
-  // complete in order) and its scores; the tile's registers are free after it
-  auto scores = [&](const uint4* kd, const uint4* vd) -> f32x4 {
+  // keys [k_lo, k_hi) of sequence b (k_lo a multiple of 16); the result goes
+  // to the output (slot < 0) or to workspace slot `slot`
+  auto piece = [&](int64_t b, int64_t k_lo, int64_t k_hi, int64_t slot) {
+    const int ntiles = k_hi > k_lo ? (int)((k_hi - k_lo + 15) / 16) : 0;
+    // query fragments (B operand of S^T): lane holds head column lane % 16,
+    // dims 32 s + 8 grp .. +7; kept in LDS to leave registers for two tiles
+    // in flight (the previous piece's reads of them were issued earlier by
+    // this wave, and LDS operations of a wave complete in order)
+    {
+      const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_ss + (int64_t)head * a.q_sh + 8 * grp;
+      // a negative scale is folded into q (an exact sign flip), a zero scale
+      // is q = 0 with c = 1 (equal weights), so the softmax below has c > 0
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
-      *reinterpret_cast<uint4*>(&vs[row * LDV + 8 * ch]) = vd[i];
+      for (int s = 0; s < NKS; ++s) {
+        const v8 qv = hvalid ? *reinterpret_cast<const v8*>(qp + 32 * s) : v8{};
+        qs[s * 64 + lane] = a.c > 0.f ? qv : (a.c < 0.f ? -qv : v8{});
+      }
     }
-    // the query fragments are re-read from LDS on every tile (an opaque index
-    // keeps them from being hoisted into registers)
-    int qo = lane;
-    asm volatile("" : "+v"(qo));
-    f32x4 s = f32x4{};
+
+    // block id of tile t's page (PAGE16), -1 past the range or for an entry
+    // outside [0, num_blocks)
+    // (PAGE16: the sequence's table row is found once; a tile is 16-key
+    // group g0 + t, in page g / gpp at slot 16 (g % gpp); key positions,
+    // table columns and block-offset products fit 32 bits, which the
+    // launcher checks, so no 64-bit division or product is left per tile)
+    const void* trow = PAGE16 ? reinterpret_cast<const char*>(a.tab.table) +
+                                    (a.tab.is64 ? 8 : 4) * (b * a.tab.row_stride)
+                              : nullptr;
+    const uint32_t gpp = PAGE16 ? (uint32_t)a.tab.page / 16u : 1u;
+    const uint32_t g0 = (uint32_t)k_lo / 16u;
+    auto tile_block = [&](int t) -> int64_t {
+      if (!PAGE16 || t >= ntiles) return -1;
+      const uint32_t g = g0 + (uint32_t)t;
+      const uint32_t col = gpp == 1u ? g : g / gpp;
+      const int64_t blk = load_index_scalar(trow, col, a.tab.is64);
+      return blk >= 0 && blk < a.tab.num_blocks ? blk : -1;
+    };
+    // row r of tile t
+    auto row_ptr = [&](const KvSource& src, int t, int64_t blk, int r) -> const char* {
+      const int64_t j = k_lo + 16 * (int64_t)t + r;
+      if (j >= k_hi) return nullptr;
+      if (PAGE16) {
+        if (blk < 0) return nullptr;
+        return src.base + blk * src.sb + (j % a.tab.page) * src.st + kvh * src.sh;
+      }
+      return kv_row<true>(src, a.tab, b, 0, j, kvh);
+    };
+    auto load_tile = [&](int t, int64_t blk, uint4* kd, uint4* vd) {
+      if (PAGE16) {
+        // one page per tile: buffer loads through a descriptor of this kv
+        // head's rows of the page (32-bit offsets, rows past the range read 0)
+        const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;
+        const int32_t nv = t < ntiles ? (int32_t)((uint32_t)k_hi - j0) : 0;
+        const uint32_t nvalid = blk < 0 ? 0u : (uint32_t)(nv < 16 ? nv : 16);
+        const uint32_t g = g0 + (uint32_t)t;
+        const uint32_t r0 = gpp == 1u ? 0u : 16u * (g - (g / gpp) * gpp);
+        const uint64_t bb = blk < 0 ? 0u : (uint32_t)blk;
+        // the ranges end after the tile's valid rows in the page, so the
+        // rows past them read as zero with no test per row
+        const uint32_t kst = (uint32_t)a.k.st, vst = (uint32_t)a.v.st;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kvk + bb * ksb), 0, (r0 + nvalid) * kst, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kvv + bb * vsb), 0, (r0 + nvalid) * vst, 0x00020000);
+        const uint32_t ko = (r0 + (uint32_t)(lane & 15)) * kst + 16u * grp;
 #pragma unroll
-    for (int k = 0; k < NKS; ++k) s = M::m16k32(__builtin_bit_cast(v8, kd[k]), qs[k * 64 + qo], s);
-    return s;
-  };
-  // second half: softmax of the scores (lane holds head column lane % 16,
-  // keys 4 grp + r of the tile) and O^T += V^T P^T
-  auto accumulate = [&](int t, f32x4 s) {
-    const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;  // (key positions fit 32 bits)
+        for (int s = 0; s < NKS; ++s)
+          kd[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64u * s, 0, 0));
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (j0 + 4u * grp + r >= (uint32_t)k_hi) s[r] = -INFINITY;
-    // maximum of this lane's 4 keys (c > 0; masked scores are -inf and give
-    // p = 0).  A head's 16 keys of the tile lie in the four 16-lane groups,
-    // which share one base: it moves only when some lane's keys exceed it by
-    // 2^8, and then to the maximum over the four lanes, taken only on that
-    // rare path (the same decisions and bases as taking it every tile)
-    const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    if (__builtin_amdgcn_ballot_w64(mx * c > m_used + 8.f) != 0) {
-      float mg = fmaxf(mx, __shfl_xor(mx, 16));
-      mg = fmaxf(mg, __shfl_xor(mg, 32));
-      const float mn = fmaxf(m_used, mg * c);
-      const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
+        for (int i = 0; i < NLD; ++i) {
+          const uint32_t cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+          vd[i] =
+              __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, (r0 + row) * vst + 16u * ch, 0, 0));
+        }
+        return;
+      }
+      {
+        const char* pk = row_ptr(a.k, t, blk, lane & 15);
 #pragma unroll
-      for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
-      lsum *= alpha;
-      m_used = mn;
-      nb = mn == -INFINITY ? 0.f : -mn;
+        for (int s = 0; s < NKS; ++s)
+          kd[s] = pk ? *reinterpret_cast<const uint4*>(pk + 2 * (32 * s + 8 * grp)) : uint4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+        const char* pv = row_ptr(a.v, t, blk, row);
+        vd[i] = pv ? *reinterpret_cast<const uint4*>(pv + 16 * ch) : uint4{0, 0, 0, 0};
+      }
+    };
+
+    f32x4 oacc[NDT];
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) oacc[d] = f32x4{};
+    float m_used = -INFINITY, lsum = 0.f;
+    float nb = 0.f;  // -m_used, or 0 while m_used is -inf (the exponent offset)
+
+    // first half of a tile: its V rows to LDS (the previous tile's transposed
+    // reads were issued earlier by this wave, and LDS operations of a wave
+    // complete in order) and its scores; the tile's registers are free after it
+    auto scores = [&](const uint4* kd, const uint4* vd) -> f32x4 {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        const int cc = lane + 64 * i, row = cc / CH, ch = cc % CH;
+        *reinterpret_cast<uint4*>(&vs[row * LDV + 8 * ch]) = vd[i];
+      }
+      // the query fragments are re-read from LDS on every tile (an opaque
+      // index keeps them from being hoisted into registers)
+      int qo = lane;
+      asm volatile("" : "+v"(qo));
+      f32x4 s = f32x4{};
+#pragma unroll
+      for (int k = 0; k < NKS; ++k) s = M::m16k32(__builtin_bit_cast(v8, kd[k]), qs[k * 64 + qo], s);
+      return s;
+    };
+    // second half: softmax of the scores (lane holds head column lane % 16,
+    // keys 4 grp + r of the tile) and O^T += V^T P^T
+    auto accumulate = [&](int t, f32x4 s) {
+      const uint32_t j0 = (uint32_t)k_lo + 16u * (uint32_t)t;  // (key positions fit 32 bits)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (j0 + 4u * grp + r >= (uint32_t)k_hi) s[r] = -INFINITY;
+      // maximum of this lane's 4 keys (c > 0; masked scores are -inf and give
+      // p = 0).  A head's 16 keys of the tile lie in the four 16-lane groups,
+      // which share one base: it moves only when some lane's keys exceed it
+      // by 2^8, and then to the maximum over the four lanes, taken only on
+      // that rare path (the same decisions and bases as taking it every tile)
+      const float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      if (__builtin_amdgcn_ballot_w64(mx * c > m_used + 8.f) != 0) {
+        float mg = fmaxf(mx, __shfl_xor(mx, 16));
+        mg = fmaxf(mg, __shfl_xor(mg, 32));
+        const float mn = fmaxf(m_used, mg * c);
+        const float alpha = mn == -INFINITY ? 1.f : exp2_fast(m_used - mn);
+#pragma unroll
+        for (int d = 0; d < NDT; ++d) oacc[d] *= alpha;
+        lsum *= alpha;
+        m_used = mn;
+        nb = mn == -INFINITY ? 0.f : -mn;
+      }
+      v4 pf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = exp2_fast(__builtin_fmaf(s[r], c, nb));
+        lsum += p;
+        pf[r] = (T)p;
+      }
+      // V^T fragments: lane holds dv 16 d + lane % 16, keys 4 grp + 0..3
+      const int j16 = lane & 15;
+      const T* vp = vs + (4 * grp + (j16 >> 2)) * LDV + 4 * (j16 & 3);
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) oacc[d] = M::m16k16(tr4<v4>(vp + 16 * d), pf, oacc[d]);
+    };
+
+    // two tiles in flight: buffers A (even tiles) and B (odd tiles); block
+    // ids are looked up two tiles before their loads are issued.  Loads are
+    // issued unconditionally (a tile past the range reads zeros and its keys
+    // are masked), so no branch makes the compiler drain the loads in flight.
+    uint4 kA[NKS], kB[NKS];
+    uint4 vA[NLD], vB[NLD];
+    int64_t bA = tile_block(2), bB = tile_block(3);
+    load_tile(0, tile_block(0), kA, vA);
+    load_tile(1, tile_block(1), kB, vB);
+    for (int t = 0; t < ntiles; t += 2) {
+      f32x4 s = scores(kA, vA);
+      load_tile(t + 2, bA, kA, vA);
+      bA = tile_block(t + 4);
+      accumulate(t, s);
+      s = scores(kB, vB);
+      load_tile(t + 3, bB, kB, vB);
+      bB = tile_block(t + 5);
+      accumulate(t + 1, s);
     }
-    v4 pf;
+
+    float lt = lsum + __shfl_xor(lsum, 16);
+    lt += __shfl_xor(lt, 32);
+    if (!hvalid) return;
+    if (slot < 0) {
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + 4 * grp;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float p = exp2_fast(__builtin_fmaf(s[r], c, nb));
-      lsum += p;
-      pf[r] = (T)p;
+      for (int d = 0; d < NDT; ++d) {
+        v4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (T)(oacc[d][e] * inv);
+        *reinterpret_cast<v4*>(op + 16 * d) = ov;
+      }
+    } else {
+      float* pp = a.part + (slot * a.Hq + head) * (int64_t)(D + 4);
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) *reinterpret_cast<f32x4*>(pp + 16 * d + 4 * grp) = oacc[d];
+      if (grp == 0) {
+        pp[D] = m_used;
+        pp[D + 1] = lt;
+      }
     }
-    // V^T fragments: lane holds dv 16 d + lane % 16, keys 4 grp + 0..3
-    const int j16 = lane & 15;
-    const T* vp = vs + (4 * grp + (j16 >> 2)) * LDV + 4 * (j16 & 3);
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) oacc[d] = M::m16k16(tr4<v4>(vp + 16 * d), pf, oacc[d]);
   };
 
-  // two tiles in flight: buffers A (even tiles) and B (odd tiles); block ids
-  // are looked up two tiles before their loads are issued.  Loads are issued
-  // unconditionally (a tile past the range reads zeros and its keys are
-  // masked), so no branch makes the compiler drain the loads in flight.
-  uint4 kA[NKS], kB[NKS];
-  uint4 vA[NLD], vB[NLD];
-  int64_t bA = tile_block(2), bB = tile_block(3);
-  load_tile(0, tile_block(0), kA, vA);
-  load_tile(1, tile_block(1), kB, vB);
-  for (int t = 0; t < ntiles; t += 2) {
-    f32x4 s = scores(kA, vA);
-    load_tile(t + 2, bA, kA, vA);
-    bA = tile_block(t + 4);
-    accumulate(t, s);
-    s = scores(kB, vB);
-    load_tile(t + 3, bB, kB, vB);
-    bB = tile_block(t + 5);
-    accumulate(t + 1, s);
+  // with one split, unit z is sequence z; else unit u holds the batch's
+  // prices [x0, x1) (they fit 31 bits, which the entry point checks)
+  constexpr int32_t SP = kDecodeStartPrice;
+  int32_t b = blockIdx.z, x0 = 0, x1 = 0, qb = 0;
+  if (a.splits > 1) {
+    const int64_t U = (int64_t)a.B * a.units;
+    const int64_t u = (int64_t)blockIdx.z * a.units + blockIdx.x;
+    if (a.prices_inline) {
+      // small batch: every wave sums the prices itself (a lane per sequence,
+      // 64 at a time), then finds the sequence holding price x0 in a second
+      // pass over the exclusive prefix; the first unit's first wave also
+      // writes the prefix for the combine
+      auto price = [&](int32_t i) -> int32_t {
+        if (i >= a.B) return 0;
+        const int32_t t = (int32_t)((clamp64(load_index(a.ctx, i, a.ctx64), 0, cap) + 15) / 16);
+        return t > 0 ? t + SP : 0;
+      };
+      int32_t tot = 0;
+      for (int32_t c0 = 0; c0 < a.B; c0 += 64) tot += price(c0 + lane);
+#pragma unroll
+      for (int d = 1; d < 64; d *= 2) tot += __shfl_xor(tot, d);
+      tot = __builtin_amdgcn_readfirstlane(tot);
+      x0 = (int32_t)(u * tot / U);
+      x1 = (int32_t)((u + 1) * tot / U);
+      const bool writer = u == 0 && blockIdx.y == 0 && wv == 0;
+      if (writer && lane == 0) a.prices[a.B] = tot;
+      if (x0 >= x1 && !writer) return;  // an empty unit (a smaller total than U): no piece
+      int32_t run = 0;
+      for (int32_t c0 = 0; c0 < a.B; c0 += 64) {
+        const int32_t p = price(c0 + lane);
+        int32_t inc = p;
+#pragma unroll
+        for (int d = 1; d < 64; d *= 2) {
+          const int32_t y = __shfl_up(inc, d);
+          if (lane >= d) inc += y;
+        }
+        const int32_t ex = run + inc - p;  // Q of sequence c0 + lane
+        if (writer && c0 + lane < a.B) a.prices[c0 + lane] = ex;
+        // the lanes with Q <= x0 are a prefix of the chunk's sequences
+        const int32_t cnt = (int32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(c0 + lane < a.B && ex <= x0));
+        if (cnt > 0) {
+          b = c0 + cnt - 1;
+          qb = __builtin_amdgcn_readlane(ex, cnt - 1);
+        }
+        run += __builtin_amdgcn_readlane(inc, 63);
+        if (cnt < 64 && !writer) break;  // (the answer is in this chunk)
+      }
+      if (x0 >= x1) return;
+    } else {
+      const int64_t Pt = load_index_scalar(a.prices, a.B, false);
+      x0 = (int32_t)(u * Pt / U);
+      x1 = (int32_t)((u + 1) * Pt / U);
+      if (x0 >= x1) return;  // an empty unit (a smaller total than U): no piece
+      // the sequence holding price x0: the last b < B with Q[b] <= x0 (Q[0] =
+      // 0), by a 64-ary search over the prefix (one probe per lane per
+      // round, Q[lo] <= x0 throughout)
+      int32_t lo = 0, hi = a.B;
+      while (hi - lo > 64) {
+        const int32_t step = (hi - lo + 63) / 64;
+        const int32_t idx = lo + lane * step;
+        const bool le = idx < hi && a.prices[idx] <= x0;
+        lo += ((int32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1) * step;
+        hi = lo + step < hi ? lo + step : hi;
+      }
+      const int32_t idx = lo + lane;
+      const bool le = idx < hi && a.prices[idx] <= x0;
+      b = __builtin_amdgcn_readfirstlane(lo + (int32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1);
+      qb = (int32_t)load_index_scalar(a.prices, b, false);
+    }
   }
-
-  float lt = lsum + __shfl_xor(lsum, 16);
-  lt += __shfl_xor(lt, 32);
-  if (!hvalid) return;
-  if (a.splits == 1) {
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + 4 * grp;
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) {
-      v4 ov;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ov[e] = (T)(oacc[d][e] * inv);
-      *reinterpret_cast<v4*>(op + 16 * d) = ov;
+  for (;;) {
+    const int64_t L = clamp64(load_index(a.ctx, b, a.ctx64), 0, cap);
+    // keys of the piece: the whole sequence (one split; a zero row when L =
+    // 0), or its tiles whose prices lie in the unit's range
+    int32_t qn = 0;
+    int64_t k_lo = 0, k_hi = L, slot = -1;
+    if (a.splits > 1) {
+      const int32_t tb = (int32_t)((L + 15) / 16);  // the sequence's tiles
+      qn = qb + (tb > 0 ? tb + SP : 0);
+      const int32_t r0 = x0 - qb - SP, r1 = x1 - qb - SP;
+      const int32_t t0 = r0 < 0 ? 0 : (r0 > tb ? tb : r0), t1 = r1 < 0 ? 0 : (r1 > tb ? tb : r1);
+      k_lo = 16 * (int64_t)t0;
+      k_hi = 16 * (int64_t)t1 < L ? 16 * (int64_t)t1 : L;
+      slot = (int64_t)b + (int64_t)blockIdx.z * a.units + blockIdx.x;
     }
-  } else {
-    float* pp = a.part + ((b * a.Hq + head) * a.splits + split) * (int64_t)(D + 4);
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) *reinterpret_cast<f32x4*>(pp + 16 * d + 4 * grp) = oacc[d];
-    if (grp == 0) {
-      pp[D] = m_used;
-      pp[D + 1] = lt;
-    }
+    if (k_hi > k_lo || slot < 0) piece(b, k_lo, k_hi, slot);
+    if (slot < 0 || qn >= x1) break;
+    ++b;
+    qb = qn;
   }
 }
 
-// Merge of the split partials of one (sequence, query head): 64 threads,
-// D / 64 output elements each.
+// Merge of the pieces of one (sequence, query head): one wave, D / 64
+// output elements per lane.  Sequence b's tiles, at prices [Q_b + start,
+// Q_{b+1}), lie in units u0 = unit(Q_b + start) .. u1 = unit(Q_{b+1} - 1),
+// unit(x) = ((x + 1) U - 1) / Q_B (the u with u Q_B / U <= x < (u+1) Q_B / U);
+// a unit with an empty price range (only when Q_B < U) holds no piece.  Piece
+// (b, u) is workspace slot b + u.  The pieces are taken 64 at a time, lane i
+// reading piece i's maximum and row sum, so their loads are in flight
+// together; the running maximum carries over between groups of 64.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void attn_decode_combine_kernel(const DecodeArgs a) {
   const int64_t bh = blockIdx.x;  // b * Hq + head
   const int64_t b = bh / a.Hq;
   const int head = (int)(bh % a.Hq);
+  const int lane = threadIdx.x;
   constexpr int PS = D + 4;
-  const float* pp = a.part + bh * a.splits * (int64_t)PS;
-  const int64_t L = clamp64(load_index(a.ctx, b, a.ctx64), 0, a.tab.cols * a.tab.page);
-  int64_t nsp = (L + a.chunk - 1) / a.chunk;
-  const int nsplit = (int)(nsp < 1 ? 1 : (nsp > a.splits ? a.splits : nsp));
-  float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, pp[s * PS + D]);
   constexpr int E = D / 64;
+  T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + E * lane;
+  const int64_t U = (int64_t)a.B * a.units;
+  const int64_t Pt = load_index_scalar(a.prices, a.B, false), qb = load_index_scalar(a.prices, b, false),
+                qn = load_index_scalar(a.prices, b + 1, false);
   float acc[E] = {};
   float l = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float ms = pp[s * PS + D];
-    if (ms == -INFINITY) continue;
-    const float wgt = exp2_fast(ms - mx);
-    l += wgt * pp[s * PS + D + 1];
+  if (qn > qb) {  // (else no keys: a zero row)
+    const int64_t u0 = ((qb + kDecodeStartPrice + 1) * U - 1) / Pt, u1 = (qn * U - 1) / Pt;
+    const bool all_units = Pt >= U;  // every unit has a price range
+    const float* base = a.part + ((b + u0) * a.Hq + head) * (int64_t)PS;
+    const int64_t rs = (int64_t)a.Hq * PS;  // one slot further
+    float mx = -INFINITY;
+    for (int64_t c0 = 0; c0 <= u1 - u0; c0 += 64) {
+      const int64_t i = c0 + lane, u = u0 + i;
+      const bool ok = u <= u1 && (all_units || (u + 1) * Pt / U > u * Pt / U);
+      const float mi = ok ? base[i * rs + D] : -INFINITY;
+      const float li = ok ? base[i * rs + D + 1] : 0.f;
+      float cm = mi;
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] += wgt * pp[s * PS + E * threadIdx.x + e];
+      for (int d = 1; d < 64; d *= 2) cm = fmaxf(cm, __shfl_xor(cm, d));
+      const float mn = fmaxf(mx, cm);
+      if (mn == -INFINITY) continue;
+      const float sc = exp2_fast(mx - mn);  // (0 while mx is -inf)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] *= sc;
+      l *= sc;
+      mx = mn;
+      const float wi = mi == -INFINITY ? 0.f : exp2_fast(mi - mx);
+      float ls = wi * li;
+#pragma unroll
+      for (int d = 1; d < 64; d *= 2) ls += __shfl_xor(ls, d);
+      l += ls;
+      const int cnt = u1 - u0 + 1 - c0 < 64 ? (int)(u1 - u0 + 1 - c0) : 64;
+#pragma unroll 4
+      for (int j = 0; j < cnt; ++j) {
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wi), j));
+        const float* pp = base + (c0 + j) * rs + E * lane;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float v = pp[e];
+          acc[e] += wj == 0.f ? 0.f : wj * v;  // (an empty unit's slot holds stale data)
+        }
+      }
+    }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* op = reinterpret_cast<T*>(a.o) + b * a.o_ss + (int64_t)head * a.o_sh + E * threadIdx.x;
 #pragma unroll
   for (int e = 0; e < E; ++e) op[e] = (T)(acc[e] * inv);
 }
@@ -970,8 +1142,13 @@ int heads_per_group(int R) { return R % 4 == 0 ? 4 : (R % 2 == 0 ? 2 : 1); }
 template <typename T, int D>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t st) {
   const int hgroups = (a.Hq / a.Hkv + 15) / 16;
-  const dim3 grid((unsigned)a.splits, (unsigned)(a.Hkv / a.kvw * hgroups), (unsigned)a.B);
+  const dim3 grid((unsigned)(a.splits > 1 ? a.units : 1), (unsigned)(a.Hkv / a.kvw * hgroups), (unsigned)a.B);
   const size_t lds = (size_t)a.kvw * decode_lds_per_wave<T, D>();
+  if (a.splits > 1 && !a.prices_inline) {
+    attn_decode_prices_kernel<<<dim3(1), dim3(1024), 0, st>>>(a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (a.tab.page % 16 == 0 && a.k.sb < (int64_t(1) << 32) && a.v.sb < (int64_t(1) << 32) &&
       a.tab.cols * a.tab.page < (int64_t(1) << 31) && a.tab.num_blocks < (int64_t(1) << 31))
     hipLaunchKernelGGL((attn_decode_kernel<T, D, true>), grid, dim3(64 * a.kvw), lds, st, a);
@@ -1071,6 +1248,8 @@ hipError_t attn_decode_scratch(hipStream_t st, float** ptr) {
   return hipSuccess;
 }
 
+int32_t attn_decode_start_price() { return kDecodeStartPrice; }
+
 hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, const gdn_tensor* vc,
                                     const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
                                     int32_t splits, float scale, hipStream_t st) {
@@ -1087,17 +1266,21 @@ hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, c
   a.ctx = ctx->data;
   a.ctx64 = ctx->dtype == GDN_DTYPE_I64;
   a.tab = paged_table(tab, kc);
-  a.part = workspace;
   a.B = (int32_t)q->shape[0];
   a.Hq = (int32_t)q->shape[1];
   a.Hkv = (int32_t)kc->shape[2];
   a.splits = splits;
   a.kvw = a.Hkv % 4 == 0 ? 4 : (a.Hkv % 2 == 0 ? 2 : 1);
   a.c = scale * kLog2e;
-  {
-    const int64_t cap = a.tab.cols * (int64_t)a.tab.page;
-    const int64_t per = (cap + splits - 1) / splits;
-    a.chunk = per < 16 ? 16 : (per + 15) / 16 * 16;
+  if (splits > 1) {
+    // workspace: the pieces' partials, B + U = B splits slots x Hq rows,
+    // then the price prefix
+    a.units = splits - 1;
+    a.part = workspace;
+    a.prices = reinterpret_cast<int32_t*>(workspace + (int64_t)a.B * splits * a.Hq * (q->shape[2] + 4));
+    // up to 1,024 sequences every decode wave sums the prices itself (16
+    // loads per lane) instead of waiting for a launch that writes them
+    a.prices_inline = a.B <= 1024;
   }
   const int D = (int)q->shape[2];
   if (q->dtype == GDN_DTYPE_BF16) {

@@ -42,6 +42,7 @@ hipError_t attn_paged_decode_launch(const gdn_tensor* q, const gdn_tensor* kc, c
                                     const gdn_tensor* tab, const gdn_tensor* ctx, gdn_tensor* out, float* workspace,
                                     int32_t splits, float scale, hipStream_t st);
 hipError_t attn_decode_scratch(hipStream_t st, float** ptr);
+int32_t attn_decode_start_price();
 hipError_t hbm_stream_copy_launch(const void* src, void* dst, int64_t nbytes, int32_t blocks, hipStream_t st);
 
 #define GDN_EXPORT extern "C" __attribute__((visibility("default")))
@@ -499,7 +500,9 @@ GDN_EXPORT int paged_attention_prefill(const gdn_tensor* q, const gdn_tensor* k_
 GDN_EXPORT int64_t paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim,
                                                          int32_t num_splits) {
   if (num_seqs < 0 || num_q_heads < 0 || head_dim < 0 || num_splits <= 1) return 0;
-  return num_seqs * num_q_heads * (int64_t)num_splits * (head_dim + 4);
+  // B splits piece slots (B sequences + B (splits - 1) units) of Hq rows of
+  // D + 4 floats, then the B + 1 int32 price prefix, rounded up to 16 bytes
+  return num_seqs * (int64_t)num_splits * num_q_heads * (head_dim + 4) + (num_seqs + 1 + 3) / 4 * 4;
 }
 
 namespace {
@@ -515,6 +518,11 @@ int check_paged_decode(const gdn_tensor* q, const gdn_tensor* k_cache, const gdn
   if (num_splits < 1 || num_splits > kMaxDecodeSplits) return GDN_ERR_RANGE;
   const int64_t Hkv = k_cache->shape[2], R = q->shape[1] / Hkv;
   if (B > kMaxGridYZ || Hkv * ((R + 15) / 16) > kMaxGridYZ) return GDN_ERR_RANGE;
+  // the split decode prices the batch (16-key tiles plus a start price per
+  // sequence) in 32 bits
+  if (num_splits > 1 &&
+      B * ((block_tables->shape[1] * k_cache->shape[1] + 15) / 16 + attn_decode_start_price()) >= (int64_t(1) << 31))
+    return GDN_ERR_RANGE;
   // one page of one kv head is addressed with 32-bit byte offsets below 2^31
   const int64_t es = elem_size(k_cache->dtype);
   if (k_cache->shape[1] * std::max(k_cache->stride[1], v_cache->stride[1]) * es >= (int64_t(1) << 31))

@@ -38,7 +38,8 @@ def _finish(out, o):
 
 
 _DECODE_MIN_SPLIT_KEYS = 256
-_DECODE_TARGET_WAVES = 2048
+_DECODE_TARGET_WAVES = 512   # unit x kv-head waves aimed at with splits
+_DECODE_SPLIT_ROWS = 2048    # (sequence, kv head) rows from which one split is enough
 _DECODE_MAX_SPLITS = 256
 
 
@@ -102,17 +103,24 @@ def _padded_prefill(q, k, v, cu_seqlens, scale, head_dim, head_v_dim, is_causal,
 
 
 def decode_num_splits(num_seqs: int, num_q_heads: int, num_kv_heads: int, capacity: int) -> int:
-    """Key splits of the decode launch.  Split s covers keys [s c, (s+1) c) of
-    the block table's ``capacity`` (max_blocks x page) with c = capacity /
-    splits; splits past a sequence's length exit at once.  Enough splits for
-    about 2048 waves (8 per CU) over the batch's (sequence, kv head) rows,
-    but at least 256 keys per split and at most 256 splits: each split costs
-    a partial-result write and read, and on the batch-256 workload 4 splits
-    of 1024 keys beat 16 of 256."""
+    """Splits of the decode launch.  With num_splits > 1 the kernel deals the
+    batch's 16-key tiles evenly over num_seqs x (num_splits - 1) units
+    (whatever the context lengths), and each unit's waves write partials that
+    a second launch merges; with one split a wave streams a whole sequence.
+    Balanced units saturate HBM from about 512 waves (unit x kv head x
+    query-head group) on; more waves only add partials and concurrent page
+    streams (256 sequences of U[512, 4096] keys, 2 kv heads: 256 units 232
+    us, 512 units 245, 1,024 units 245; 64 of U[2k, 32k]: 192 units 397 us,
+    1,024 units 429).  So: about 512 waves, at least one unit per sequence
+    (one split leaves ragged batches unbalanced), one split once the batch
+    alone has 2048 rows, and at least 256 keys of the table's capacity per
+    unit."""
     rows = max(1, num_seqs * num_kv_heads * ((num_q_heads // max(num_kv_heads, 1) + 15) // 16))
-    by_waves = -(-_DECODE_TARGET_WAVES // rows)
+    if rows >= _DECODE_SPLIT_ROWS:
+        return 1
+    units = max(1, round(_DECODE_TARGET_WAVES / rows))
     by_keys = -(-max(capacity, 1) // _DECODE_MIN_SPLIT_KEYS)
-    return max(1, min(_DECODE_MAX_SPLITS, by_waves, by_keys))
+    return max(1, min(_DECODE_MAX_SPLITS, 1 + min(units, by_keys)))
 
 
 def paged_flash_attention_decode(

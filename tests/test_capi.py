@@ -336,7 +336,7 @@ def _paged_attn_args(B=2, Hq=4, Hkv=2, Dh=128, blocks=5, page=16, cols=3, dtype=
     return dict(q=torch.zeros(B, Hq, Dh, dtype=dtype), kc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype),
                 vc=torch.zeros(blocks, page, Hkv, Dh, dtype=dtype), tab=torch.zeros(B, cols, dtype=torch.int32),
                 ctx=torch.ones(B, dtype=torch.int32), out=torch.zeros(B, Hq, Dh, dtype=dtype),
-                ws=torch.zeros(B * Hq * 4 * (Dh + 4)), splits=4)
+                ws=torch.zeros(_lib.load().paged_attention_decode_workspace_size(B, Hq, Dh, 4)), splits=4)
 
 
 def _call_paged_decode(a):
@@ -355,12 +355,12 @@ def _call_paged_decode(a):
         (lambda a: a.update(ctx=torch.zeros(3, dtype=torch.int32)), "SHAPE"),
         (lambda a: a.update(ws=torch.zeros(10)), "SHAPE"),
         (lambda a: a.update(ws=None), "NULL"),
-        (lambda a: a.update(ws=torch.zeros(2 * 4 * 4 * 132, dtype=torch.float16)), "DTYPE"),
+        (lambda a: a.update(ws=torch.zeros(a["ws"].numel(), dtype=torch.float16)), "DTYPE"),
         (lambda a: a.update(tab=torch.zeros(2, 3)), "DTYPE"),
         (lambda a: a.update(tab=torch.zeros(3, 2, dtype=torch.int32).t()), "STRIDE"),
         (lambda a: a.update(splits=0), "RANGE"),
         (lambda a: a.update(splits=257), "RANGE"),
-        (lambda a: a.update(ws=torch.zeros(2 * 4 * 4 * 132 + 1)[1:]), "ALIGN"),
+        (lambda a: a.update(ws=torch.zeros(a["ws"].numel() + 1)[1:]), "ALIGN"),
     ],
 )
 def test_paged_decode_validation(mutate, code):
@@ -387,10 +387,30 @@ def test_paged_prefill_validation():
     assert call(cu=torch.tensor([0.0, 2.0, 5.0])) == ERR["DTYPE"]
 
 
+@cpu_only
+@pytest.mark.parametrize("cols, splits, refused", [(2**30, 4, True), (2**30, 1, False), (2**29 - 4, 4, False)])
+def test_paged_decode_price_range(cols, splits, refused):
+    """The split decode prices the batch (16-key tiles of the table's capacity
+    plus a start price of 2 per sequence) in 32 bits: 2 sequences x 2^30
+    columns of 16 keys exceed 2^31 and are refused (RANGE) before any HIP
+    call; 2^29 - 4 columns fit, and one split prices nothing (on a machine
+    without a GPU those calls get as far as the launch, which fails).  Only
+    the descriptor's column count is large: no kernel runs."""
+    a = _paged_attn_args()
+    a["splits"] = splits
+    tab = D(a["tab"])
+    tab.shape[1] = cols
+    rc = _lib.load().paged_attention_decode(D(a["q"]), D(a["kc"]), D(a["vc"]), tab, D(a["ctx"]), D(a["out"]),
+                                            D(a["ws"]), splits, 1.0, None)
+    assert (rc == ERR["RANGE"]) == refused
+    if not refused:
+        assert rc > 0  # a hipError_t from the launch
+
+
 def test_decode_workspace_size():
     lib = _lib.load()
     assert lib.paged_attention_decode_workspace_size(3, 16, 256, 1) == 0
-    assert lib.paged_attention_decode_workspace_size(3, 16, 256, 4) == 3 * 16 * 4 * 260
+    assert lib.paged_attention_decode_workspace_size(3, 16, 256, 4) == 3 * 4 * 16 * 260 + 4
 
 
 def _call_paged_decode_noalloc(a):

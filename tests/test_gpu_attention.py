@@ -186,6 +186,28 @@ def test_paged_decode(dev, ctx, Hq, Hkv, Dh, page, splits):
     assert (out[torch.tensor(ctx) == 0] == 0).all()
 
 
+@pytest.mark.parametrize(
+    "label, ctx, splits",
+    [
+        # one long sequence among many short ones: units cross many sequence
+        # ends and the long one spans many units
+        ("skewed", [5000] + [int(x) for x in torch.randint(1, 41, (300,), generator=torch.Generator().manual_seed(5))], 3),
+        # more than 1,024 sequences: the price prefix comes from its own launch
+        ("b1100", [int(x) for x in torch.randint(0, 70, (1100,), generator=torch.Generator().manual_seed(6))], 2),
+        # fewer priced tiles than units: empty units, sequences without keys
+        ("sparse", [1, 0, 0, 2, 0, 33], 16),
+    ],
+)
+def test_paged_decode_balanced_units(dev, label, ctx, splits):
+    """Split decode over units that each take an equal share of the batch's
+    priced tiles, checked against the float64 reference on every row."""
+    case = paged_case(ctx, [1] * len(ctx), page=16, seed=len(ctx), Hq=8, Hkv=2, D=64)
+    print(f"paged decode balanced units {label}: B={len(ctx)} splits={splits}", flush=True)
+    out = _decode(case, dev, splits)
+    assert_attn_close(out, _decode_ref(case))
+    assert (out[torch.tensor(ctx) == 0] == 0).all()
+
+
 def test_paged_decode_equals_paged_prefill_of_one_token(dev):
     case = paged_case([90, 33], [1, 1], seed=3, Hq=8, Hkv=2, D=128)
     a = _decode(case, dev, 3)
