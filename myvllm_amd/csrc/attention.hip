@@ -612,11 +612,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 // [Q_b + kDecodeStartPrice, Q_{b+1}), and unit u takes the tiles whose prices
 // lie in [u Q_B / U, (u+1) Q_B / U).  So every unit streams about the same
 // number of keys whatever the lengths are.  A unit crossing sequence ends
-// runs one piece per sequence, and each piece (sequence b, unit u) writes its
-// unnormalised O, running maximum and row sum to workspace slot b + u < B +
-// U (distinct for distinct pieces: a later piece has a later unit or a later
-// sequence and neither index decreases), which attn_decode_combine_kernel
-// merges.  The price prefix Q is summed by the decode waves themselves for
+// runs one piece per sequence.  A piece that is a whole sequence writes its
+// output row; any other piece (sequence b, unit u) writes its unnormalised O,
+// running maximum and row sum to workspace slot b + u < B + U (distinct for
+// distinct pieces: a later piece has a later unit or a later sequence and
+// neither index decreases), which attn_decode_combine_kernel merges.  The price prefix Q is summed by the decode waves themselves for
 // batches of up to 1,024 sequences, else by attn_decode_prices_kernel,
 // launched first.  With a page size that is a multiple of 16 a 16-key tile
 // lies in one page: its block id is one wave-uniform load, issued a tile ahead
@@ -984,9 +984,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   for (;;) {
     const int64_t L = clamp64(load_index(a.ctx, b, a.ctx64), 0, cap);
     // keys of the piece: the whole sequence (one split; a zero row when L =
-    // 0), or its tiles whose prices lie in the unit's range
+    // 0), or its tiles whose prices lie in the unit's range.  A unit that
+    // holds all of a sequence's tiles writes its output row itself (the
+    // combine finds that sequence in one unit and skips it), else the piece
+    // goes to its workspace slot.
     int32_t qn = 0;
     int64_t k_lo = 0, k_hi = L, slot = -1;
+    bool any = true;
     if (a.splits > 1) {
       const int32_t tb = (int32_t)((L + 15) / 16);  // the sequence's tiles
       qn = qb + (tb > 0 ? tb + SP : 0);
@@ -994,10 +998,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       const int32_t t0 = r0 < 0 ? 0 : (r0 > tb ? tb : r0), t1 = r1 < 0 ? 0 : (r1 > tb ? tb : r1);
       k_lo = 16 * (int64_t)t0;
       k_hi = 16 * (int64_t)t1 < L ? 16 * (int64_t)t1 : L;
-      slot = (int64_t)b + (int64_t)blockIdx.z * a.units + blockIdx.x;
+      any = t1 > t0;
+      if (t0 > 0 || t1 < tb) slot = (int64_t)b + (int64_t)blockIdx.z * a.units + blockIdx.x;
     }
-    if (k_hi > k_lo || slot < 0) piece(b, k_lo, k_hi, slot);
-    if (slot < 0 || qn >= x1) break;
+    if (any) piece(b, k_lo, k_hi, slot);
+    if (a.splits == 1 || qn >= x1) break;
     ++b;
     qb = qn;
   }
@@ -1008,7 +1013,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 // Q_{b+1}), lie in units u0 = unit(Q_b + start) .. u1 = unit(Q_{b+1} - 1),
 // unit(x) = ((x + 1) U - 1) / Q_B (the u with u Q_B / U <= x < (u+1) Q_B / U);
 // a unit with an empty price range (only when Q_B < U) holds no piece.  Piece
-// (b, u) is workspace slot b + u.  The pieces are taken 64 at a time, lane i
+// (b, u) is workspace slot b + u; a sequence inside one unit has no piece
+// there, its row was written by that unit.  The pieces are taken 64 at a time, lane i
 // reading piece i's maximum and row sum, so their loads are in flight
 // together; the running maximum carries over between groups of 64.
 template <typename T, int D>
@@ -1027,6 +1033,7 @@ __global__ __launch_bounds__(64) void attn_decode_combine_kernel(const DecodeArg
   float l = 0.f;
   if (qn > qb) {  // (else no keys: a zero row)
     const int64_t u0 = ((qb + kDecodeStartPrice + 1) * U - 1) / Pt, u1 = (qn * U - 1) / Pt;
+    if (u0 == u1) return;  // one unit held the whole sequence and wrote its row
     const bool all_units = Pt >= U;  // every unit has a price range
     const float* base = a.part + ((b + u0) * a.Hq + head) * (int64_t)PS;
     const int64_t rs = (int64_t)a.Hq * PS;  // one slot further
