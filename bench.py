@@ -60,15 +60,15 @@ PREFILL_FLOP_PER_TOKEN = 2 * (2 * CHUNK * DK * HK + (2 * CHUNK * DV + CHUNK * DK
 # nothing else).  Values from the committed profiles of the current kernels
 # (profiles/*.md, which give the commands); a kernel without an entry reports None.
 HBM_TRAFFIC_PER_LAUNCH = {
-    "gdn_chunk_prefill_kernel": 1_027_009_376,
-    "gdn_chunk_prefill_kernel/short": 3_862_119_536,
-    "gdn_recurrent_step_kernel": 1_083_281_312,
-    "causal_conv1d_varlen_kernel": 666_030_592,
-    "causal_conv1d_step_kernel": 59_315_296,
-    "gdn_decode_fused_kernel": 1_131_414_048,
-    "attn_prefill_kernel": 933_084_416,
-    "attn_decode_kernel": 1_259_544_352,  # with its combine kernel
-    "attn_paged_prefill_kernel": 821_896_192,
+    "gdn_chunk_prefill_kernel": 1_027_048_208,
+    "gdn_chunk_prefill_kernel/short": 3_853_347_984,
+    "gdn_recurrent_step_kernel": 1_083_263_120,
+    "causal_conv1d_varlen_kernel": 666_022_912,
+    "causal_conv1d_step_kernel": 59_316_992,
+    "gdn_decode_fused_kernel": 1_131_415_744,
+    "attn_prefill_kernel": 932_966_560,
+    "attn_decode_kernel": 1_257_835_584,  # with its combine kernel
+    "attn_paged_prefill_kernel": 822_067_328,
 }
 
 
