@@ -187,22 +187,27 @@ def test_paged_decode(dev, ctx, Hq, Hkv, Dh, page, splits):
 
 
 @pytest.mark.parametrize(
-    "label, ctx, splits",
+    "label, ctx, splits, page, D",
     [
         # one long sequence among many short ones: units cross many sequence
         # ends and the long one spans many units
-        ("skewed", [5000] + [int(x) for x in torch.randint(1, 41, (300,), generator=torch.Generator().manual_seed(5))], 3),
+        ("skewed", [5000] + [int(x) for x in torch.randint(1, 41, (300,), generator=torch.Generator().manual_seed(5))], 3,
+         16, 64),
         # more than 1,024 sequences: the price prefix comes from its own launch
-        ("b1100", [int(x) for x in torch.randint(0, 70, (1100,), generator=torch.Generator().manual_seed(6))], 2),
+        ("b1100", [int(x) for x in torch.randint(0, 70, (1100,), generator=torch.Generator().manual_seed(6))], 2, 16, 64),
         # fewer priced tiles than units: empty units, sequences without keys
-        ("sparse", [1, 0, 0, 2, 0, 33], 16),
+        ("sparse", [1, 0, 0, 2, 0, 33], 16, 16, 64),
+        # pages that are not a multiple of 16 (rows looked up one by one) and
+        # pages of 48 (three tiles per page), head dim 256
+        ("page7", [700, 3, 0, 129, 1000, 31], 3, 7, 256),
+        ("page48", [700, 3, 0, 129, 1000, 31], 3, 48, 256),
     ],
 )
-def test_paged_decode_balanced_units(dev, label, ctx, splits):
+def test_paged_decode_balanced_units(dev, label, ctx, splits, page, D):
     """Split decode over units that each take an equal share of the batch's
     priced tiles, checked against the float64 reference on every row."""
-    case = paged_case(ctx, [1] * len(ctx), page=16, seed=len(ctx), Hq=8, Hkv=2, D=64)
-    print(f"paged decode balanced units {label}: B={len(ctx)} splits={splits}", flush=True)
+    case = paged_case(ctx, [1] * len(ctx), page=page, seed=len(ctx), Hq=8, Hkv=2, D=D)
+    print(f"paged decode balanced units {label}: B={len(ctx)} splits={splits} page={page} D={D}", flush=True)
     out = _decode(case, dev, splits)
     assert_attn_close(out, _decode_ref(case))
     assert (out[torch.tensor(ctx) == 0] == 0).all()
