@@ -616,11 +616,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
 // output row; any other piece (sequence b, unit u) writes its unnormalised O,
 // running maximum and row sum to workspace slot b + u < B + U (distinct for
 // distinct pieces: a later piece has a later unit or a later sequence and
-// neither index decreases), which attn_decode_combine_kernel merges.  The price prefix Q is summed by the decode waves themselves for
-// batches of up to 1,024 sequences, else by attn_decode_prices_kernel,
-// launched first.  With a page size that is a multiple of 16 a 16-key tile
-// lies in one page: its block id is one wave-uniform load, issued a tile ahead
-// of the K/V loads that use it.  The kvw kv heads of a workgroup (one wave
+// neither index decreases), which attn_decode_combine_kernel merges.  The
+// price prefix Q is summed by the decode waves themselves for batches of up to
+// 1,024 sequences, else by attn_decode_prices_kernel, launched first.  With a
+// page size that is a multiple of 16 a 16-key tile lies in one page: its block
+// id is one wave-uniform load, issued a tile ahead of the K/V loads that use
+// it.  The kvw kv heads of a workgroup (one wave
 // each) read the interleaved head rows of the same cache slots at about the
 // same time, so each page is streamed as one contiguous region.
 constexpr int32_t kDecodeStartPrice = 2;
@@ -655,12 +656,12 @@ __global__ __launch_bounds__(1024) void attn_decode_prices_kernel(const DecodeAr
   const int64_t cap = a.tab.cols * a.tab.page;
   const int per = (a.B + 1023) / 1024;
   const int64_t b0 = (int64_t)tid * per;
-  auto tiles_of = [&](int64_t b) -> int32_t {
+  auto price_of = [&](int64_t b) -> int32_t {
     const int32_t t = b < a.B ? (int32_t)((clamp64(load_index(a.ctx, b, a.ctx64), 0, cap) + 15) / 16) : 0;
     return t > 0 ? t + kDecodeStartPrice : 0;
   };
   int32_t sum = 0;
-  for (int i = 0; i < per; ++i) sum += tiles_of(b0 + i);
+  for (int i = 0; i < per; ++i) sum += price_of(b0 + i);
   // inclusive scan over the wave, then over the 16 wave totals
   int32_t inc = sum;
 #pragma unroll
@@ -677,7 +678,7 @@ __global__ __launch_bounds__(1024) void attn_decode_prices_kernel(const DecodeAr
     const int64_t b = b0 + i;
     if (b >= a.B) break;
     a.prices[b] = run;
-    run += tiles_of(b);
+    run += price_of(b);
   }
   if (tid == 1023) a.prices[a.B] = base + inc;
 }
