@@ -1060,7 +1060,6 @@ __global__ __launch_bounds__(64) void attn_decode_combine_kernel(const DecodeArg
       for (int d = 1; d < 64; d *= 2) ls += __shfl_xor(ls, d);
       l += ls;
       const int cnt = u1 - u0 + 1 - c0 < 64 ? (int)(u1 - u0 + 1 - c0) : 64;
-#pragma unroll 4
       for (int j = 0; j < cnt; ++j) {
         const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wi), j));
         const float* pp = base + (c0 + j) * rs + E * lane;
