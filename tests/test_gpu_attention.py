@@ -213,6 +213,20 @@ def test_paged_decode_balanced_units(dev, label, ctx, splits, page, D):
     assert (out[torch.tensor(ctx) == 0] == 0).all()
 
 
+@pytest.mark.parametrize("B, splits", [(6, 1), (6, 3), (1100, 2)])
+def test_paged_decode_int64_indices(dev, B, splits):
+    """int64 block tables and context lengths: one split, units priced by the
+    decode waves (6 sequences) and by the separate prefix launch (1,100)."""
+    gen = torch.Generator().manual_seed(B + splits)
+    ctx = torch.randint(0, 300, (B,), generator=gen).tolist()
+    case = paged_case(ctx, [1] * B, page=16, seed=B, Hq=8, Hkv=2, D=128)
+    case.block_tables = case.block_tables.to(torch.int64)
+    case.context_lens = case.context_lens.to(torch.int64)
+    print(f"paged decode int64 indices B={B} splits={splits}", flush=True)
+    out = _decode(case, dev, splits)
+    assert_attn_close(out, _decode_ref(case))
+
+
 def test_paged_decode_equals_paged_prefill_of_one_token(dev):
     case = paged_case([90, 33], [1, 1], seed=3, Hq=8, Hkv=2, D=128)
     a = _decode(case, dev, 3)
