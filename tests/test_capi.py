@@ -407,6 +407,29 @@ def test_paged_decode_price_range(cols, splits, refused):
         assert rc > 0  # a hipError_t from the launch
 
 
+@pytest.mark.parametrize(
+    "B, Hq, Hkv, capacity, splits",
+    [
+        (256, 16, 2, 4096, 2),     # 512 (sequence, kv head) rows: one unit per sequence
+        (128, 16, 2, 4096, 3),     # 256 rows: two units per sequence
+        (64, 16, 2, 32768, 5),     # 128 rows: four
+        (16, 16, 2, 32768, 17),    # 32 rows: sixteen
+        (512, 16, 2, 2048, 2),     # 1,024 rows: still at least one unit per sequence
+        (1024, 16, 2, 1024, 1),    # 2,048 rows: one split
+        (1, 64, 2, 100000, 129),   # 32 query heads per kv head: two head groups, 4 rows, 128 units
+        (3, 16, 2, 300, 3),        # capacity 300: at most ceil(300 / 256) = 2 units per sequence
+        (1, 16, 1, 10**6, 256),    # the cap
+    ],
+)
+def test_decode_num_splits(B, Hq, Hkv, capacity, splits):
+    """The decode's default split count: about 512 unit x kv head x head
+    group waves, at least one unit per sequence below 2,048 rows, one split
+    from there, at most ceil(capacity / 256) units per sequence and 256
+    splits."""
+    from myvllm_amd.full_attention import decode_num_splits
+    assert decode_num_splits(B, Hq, Hkv, capacity) == splits
+
+
 def test_decode_workspace_size():
     lib = _lib.load()
     assert lib.paged_attention_decode_workspace_size(3, 16, 256, 1) == 0
